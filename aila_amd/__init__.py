@@ -1,1 +1,156 @@
-"""MI355X-native attention hot path for Aila (GQA + Gated DeltaNet)."""
+"""MI355X-native attention hot path for Aila (Qwen3 GQA + Gated DeltaNet).
+
+The compute lives in ``aila_amd/libaila_hip.so`` (hand-written gfx950 HIP
+kernels behind the C ABI declared in ``include/aila_hip.h``). This module
+is a thin host-side binding over that C ABI for torch device tensors: it
+checks shapes, dtypes and contiguity on the host, then passes raw device
+pointers and the current HIP stream. There is no fallback: if the library
+is missing or fails to load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libaila_hip.so")
+_lib = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+_SIGS = {
+    "aila_hip_last_error": ([], ctypes.c_char_p),
+    "aila_hip_version": ([], _I),
+    "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
+    "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                  _I, _I, _I, _I, _I, _F, _F, _P], _I),
+}
+
+
+class AilaHipError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise AilaHipError(
+                f"{LIB_PATH} not found: build it with `python -m aila_amd.build`")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (argt, rest) in _SIGS.items():
+            f = getattr(l, name)
+            f.argtypes = argt
+            f.restype = rest
+        _lib = l
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().aila_hip_last_error().decode(errors="replace")
+        raise AilaHipError(f"{what} failed ({rc}): {msg}")
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t, dtype, shape, name, align=16):
+    import torch
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name} must be {align}-byte aligned")
+    del torch
+
+
+# ----------------------------------------------------------------- GQA ----
+def gqa_decode_workspace_size(B: int, Hq: int, D: int) -> int:
+    return int(lib().aila_hip_gqa_decode_workspace_size(B, Hq, D))
+
+
+def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
+               seq_lens=None, stream=None):
+    """q [B,Hq,D] bf16; k_cache/v_cache [B,Hkv,max_seq,D] bf16 -> out [B,Hq,D].
+
+    ``workspace``: uint8 device tensor of >= gqa_decode_workspace_size bytes
+    enables split-K; None runs the single-pass kernel. ``seq_lens``: optional
+    int32 [B] device tensor of per-sequence lengths (<= cached_len)."""
+    import torch
+    B, Hq, D = q.shape
+    Hkv, max_seq = k_cache.shape[1], k_cache.shape[2]
+    _need(q, torch.bfloat16, (B, Hq, D), "q")
+    _need(k_cache, torch.bfloat16, (B, Hkv, max_seq, D), "k_cache")
+    _need(v_cache, torch.bfloat16, (B, Hkv, max_seq, D), "v_cache")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.bfloat16, (B, Hq, D), "out")
+    ws_bytes = 0
+    if workspace is not None:
+        if not workspace.is_cuda or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous device tensor")
+        ws_bytes = workspace.numel() * workspace.element_size()
+    if seq_lens is not None:
+        _need(seq_lens, torch.int32, (B,), "seq_lens", align=4)
+    rc = lib().aila_hip_gqa_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                   _ptr(workspace), ws_bytes, B, Hq, Hkv, D, max_seq,
+                                   int(cached_len), _ptr(seq_lens), _stream(stream))
+    _check(rc, "aila_hip_gqa_decode")
+    return out
+
+
+# ------------------------------------------------------------ DeltaNet ----
+def deltanet_decode(q, k, v, a, b, state, out=None, dt_bias=None, A_log=None,
+                    eps: float = 1e-6, scale: float | None = None, stream=None):
+    """One Gated DeltaNet step. q,k [B,Hk,dk] bf16; v [B,Hv,dv] bf16;
+    a,b [B,Hv] bf16; state [B,Hv,dk,dv] fp32 (updated in place) -> out
+    [B,Hv,dv] bf16."""
+    import torch
+    B, Hk, dk = q.shape
+    Hv, dv = v.shape[1], v.shape[2]
+    _need(q, torch.bfloat16, (B, Hk, dk), "q")
+    _need(k, torch.bfloat16, (B, Hk, dk), "k")
+    _need(v, torch.bfloat16, (B, Hv, dv), "v")
+    _need(a, torch.bfloat16, (B, Hv), "a", align=2)
+    _need(b, torch.bfloat16, (B, Hv), "b", align=2)
+    _need(state, torch.float32, (B, Hv, dk, dv), "state")
+    if dt_bias is not None:
+        _need(dt_bias, torch.bfloat16, (Hv,), "dt_bias", align=2)
+    if A_log is not None:
+        _need(A_log, torch.float32, (Hv,), "A_log", align=4)
+    if out is None:
+        out = torch.empty((B, Hv, dv), dtype=torch.bfloat16, device=q.device)
+    _need(out, torch.bfloat16, (B, Hv, dv), "out")
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    rc = lib().aila_hip_deltanet_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
+                                        _ptr(dt_bias), _ptr(A_log), _ptr(state), _ptr(out),
+                                        B, Hk, Hv, dk, dv, float(eps), float(scale),
+                                        _stream(stream))
+    _check(rc, "aila_hip_deltanet_decode")
+    return out

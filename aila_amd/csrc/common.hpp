@@ -1,0 +1,126 @@
+// Shared device helpers for the gfx950 kernels: bf16 storage type and
+// conversions, MFMA operand vector types, DPP row reductions and the
+// C-ABI error plumbing used by every entry point.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include "aila_hip.h"
+
+namespace aila {
+
+// bf16 is carried as its 16-bit pattern; arithmetic is always fp32.
+typedef uint16_t bf16;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf2f(bf16 h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (quiet NaN preserved), identical to
+// the host oracle's orc_f32_to_bf16.
+__device__ __forceinline__ bf16 f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu))
+    return static_cast<bf16>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16>(u >> 16);
+}
+
+// Two fp32 -> packed bf16x2 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+}
+
+// Unpack 8 bf16 held in a 16-byte vector into fp32.
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(v[i] << 16);
+    f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4& v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// D = A * B + C with A 16x32, B 32x16 (bf16), C/D 16x16 fp32.
+// Lane l supplies A[l%16][8*(l/16) .. +8] and B[8*(l/16) .. +8][l%16];
+// it receives D[4*(l/16) + j][l%16] in element j.
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8_t& a,
+                                              const bf16x8_t& b,
+                                              const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---- DPP reductions inside a row of 16 lanes ---------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(
+      0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+// After these four steps every lane of a 16-lane row holds the row's
+// max / sum (each step pairs every lane with a lane of the other half of
+// the group being merged).
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_f<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp_f<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp_f<kDppRowHalfMirror>(x));
+  x = fmaxf(x, dpp_f<kDppRowMirror>(x));
+  return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f<kDppQuadXor1>(x);
+  x += dpp_f<kDppQuadXor2>(x);
+  x += dpp_f<kDppRowHalfMirror>(x);
+  x += dpp_f<kDppRowMirror>(x);
+  return x;
+}
+
+// Full 64-lane sum (DPP inside rows, then cross-row swizzles).
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float readlane_f(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+}  // namespace aila
+
+// ---- host-side error plumbing (defined in capi.hip) ---------------------
+namespace aila {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace aila
+
+#define AILA_REQUIRE(cond, ...)                                  \
+  do {                                                           \
+    if (!(cond)) return ::aila::set_error(AILA_HIP_EINVAL, __VA_ARGS__); \
+  } while (0)

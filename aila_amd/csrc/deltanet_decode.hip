@@ -1,0 +1,198 @@
+// Gated DeltaNet decode step on gfx950: a memory-bound rank-1 state update
+// that reads and writes the fp32 state exactly once.
+//
+// Reference: Qwen35HybridTextBackend::run_linear_delta_decode_gpu
+// (src/models/Qwen35HybridTextBackend.cpp:1013-1166) touches the state
+// twice (a decay pass and an update pass, 2 reads + 2 writes). Here the
+// state column slab lives in VGPRs between the two reductions.
+//
+// Work decomposition: one 256-thread workgroup per (value head, sequence,
+// 128-column slab of dv). Thread t owns columns 4*(t%32)..+3 of the slab and
+// rows (t/32)*RPT..+RPT-1 of dk (RPT = dk/8). Loads are float4 along dv, so a
+// wave reads two 512-byte row segments per instruction. The column sums
+// u = S^T k and o = S^T q are reduced over the 8 row groups with one
+// lane-swap (row groups 2w and 2w+1 share wave w) and an LDS pass over the 4
+// waves.
+#include "common.hpp"
+
+namespace aila {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kColQuads = 32;   // 128 columns per workgroup
+constexpr int kRowGroups = 8;
+
+__device__ __forceinline__ float softplus_f(float x) {
+  // Qwen35HybridTextBackend.cpp:128-132
+  if (x > 20.0f) return x;
+  if (x < -20.0f) return expf(x);
+  return log1pf(expf(x));
+}
+
+template <int DK>
+__global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k,
+    const bf16* __restrict__ v, const bf16* __restrict__ a,
+    const bf16* __restrict__ bgate, const bf16* __restrict__ dt_bias,
+    const float* __restrict__ A_log, float* __restrict__ state,
+    bf16* __restrict__ out, int Hk, int Hv, int dv, float eps, float scale) {
+  constexpr int RPT = DK / kRowGroups;  // rows per thread
+  const int hv = blockIdx.x;
+  const int bseq = blockIdx.y;
+  const int slab = blockIdx.z;
+  const int t = threadIdx.x;
+  const int cq = t % kColQuads;
+  const int rg = t / kColQuads;
+  const int col = slab * (kColQuads * 4) + cq * 4;
+  const bool active = col < dv;          // dv % 4 == 0 is required
+  const int hk = hv / (Hv / Hk);
+
+  __shared__ float s_q[DK];
+  __shared__ float s_k[DK];
+  __shared__ float s_red[2][4][kColQuads * 4];
+  __shared__ float s_norm[2][4];
+
+  float* S = state + (static_cast<size_t>(bseq) * Hv + hv) * DK * dv;
+
+  // 1. Issue the state loads first so their latency overlaps the q/k norms.
+  f32x4 s[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int row = rg * RPT + r;
+    s[r] = active ? *reinterpret_cast<const f32x4*>(S + static_cast<size_t>(row) * dv + col)
+                  : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // 2. q, k L2 norms (head_l2_norm_inplace, :138-151 / :1079-1089).
+  const bf16* qh = q + (static_cast<size_t>(bseq) * Hk + hk) * DK;
+  const bf16* kh = k + (static_cast<size_t>(bseq) * Hk + hk) * DK;
+  float sq = 0.f, sk = 0.f;
+  for (int i = t; i < DK; i += kThreads) {
+    const float qf = bf2f(qh[i]), kf = bf2f(kh[i]);
+    s_q[i] = qf;
+    s_k[i] = kf;
+    sq += qf * qf;
+    sk += kf * kf;
+  }
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  const int wave = t >> 6, lane = t & 63;
+  if (lane == 0) {
+    s_norm[0][wave] = sq;
+    s_norm[1][wave] = sk;
+  }
+  // Gates (Qwen35HybridTextBackend.cpp:1091-1099), uniform per head.
+  const size_t gi = static_cast<size_t>(bseq) * Hv + hv;
+  const float beta = 1.0f / (1.0f + expf(-bf2f(bgate[gi])));
+  const float dtb = dt_bias ? bf2f(dt_bias[hv]) : 0.0f;
+  const float negA = A_log ? -expf(A_log[hv]) : -1.0f;
+  const float decay = expf(softplus_f(bf2f(a[gi]) + dtb) * negA);
+  __syncthreads();
+  const float qn = 1.0f / sqrtf(s_norm[0][0] + s_norm[0][1] + s_norm[0][2] + s_norm[0][3] + eps);
+  const float kn = 1.0f / sqrtf(s_norm[1][0] + s_norm[1][1] + s_norm[1][2] + s_norm[1][3] + eps);
+
+  // 3. S *= decay; partial u = S^T k over this thread's rows.
+  float kr[RPT];
+  f32x4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    kr[r] = s_k[rg * RPT + r] * kn;
+    s[r] *= decay;
+    u += s[r] * kr[r];
+  }
+  // Row groups 2w and 2w+1 live in lanes [0,32) and [32,64) of wave w.
+#pragma unroll
+  for (int e = 0; e < 4; ++e) u[e] += __shfl_xor(u[e], 32);
+  if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[0][wave][cq * 4]) = u;
+  __syncthreads();
+  u = *reinterpret_cast<const f32x4*>(&s_red[0][0][cq * 4]) +
+      *reinterpret_cast<const f32x4*>(&s_red[0][1][cq * 4]) +
+      *reinterpret_cast<const f32x4*>(&s_red[0][2][cq * 4]) +
+      *reinterpret_cast<const f32x4*>(&s_red[0][3][cq * 4]);
+
+  // 4. d = (v - u) * beta ; S += k d^T ; partial o = S^T q.
+  f32x4 vv = {0.f, 0.f, 0.f, 0.f};
+  if (active) {
+    const bf16* vh = v + gi * dv + col;
+    const uint2 raw = *reinterpret_cast<const uint2*>(vh);
+    vv[0] = __uint_as_float(raw.x << 16);
+    vv[1] = __uint_as_float(raw.x & 0xffff0000u);
+    vv[2] = __uint_as_float(raw.y << 16);
+    vv[3] = __uint_as_float(raw.y & 0xffff0000u);
+  }
+  const f32x4 d = (vv - u) * beta;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const float qr = s_q[rg * RPT + r] * qn;
+    s[r] += kr[r] * d;
+    o += s[r] * qr;
+  }
+  // 5. Single write of the state.
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int row = rg * RPT + r;
+      *reinterpret_cast<f32x4*>(S + static_cast<size_t>(row) * dv + col) = s[r];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], 32);
+  if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[1][wave][cq * 4]) = o;
+  __syncthreads();
+  if (t < kColQuads && active) {
+    o = *reinterpret_cast<const f32x4*>(&s_red[1][0][cq * 4]) +
+        *reinterpret_cast<const f32x4*>(&s_red[1][1][cq * 4]) +
+        *reinterpret_cast<const f32x4*>(&s_red[1][2][cq * 4]) +
+        *reinterpret_cast<const f32x4*>(&s_red[1][3][cq * 4]);
+    o *= scale;
+    uint2 w;
+    w.x = pack_bf16x2(o[0], o[1]);
+    w.y = pack_bf16x2(o[2], o[3]);
+    *reinterpret_cast<uint2*>(out + gi * dv + col) = w;
+  }
+}
+
+}  // namespace
+}  // namespace aila
+
+extern "C" int aila_hip_deltanet_decode(const void* q, const void* k,
+                                        const void* v, const void* a,
+                                        const void* b, const void* dt_bias,
+                                        const float* A_log, float* state,
+                                        void* out, int B, int Hk, int Hv,
+                                        int dk, int dv, float eps, float scale,
+                                        void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(q && k && v && a && b && state && out, "deltanet_decode: null pointer");
+  AILA_REQUIRE(B > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0,
+               "deltanet_decode: need B, Hk, Hv > 0 and Hv %% Hk == 0 (B=%d Hk=%d Hv=%d)", B, Hk, Hv);
+  AILA_REQUIRE(dv > 0 && dv % 4 == 0, "deltanet_decode: dv must be a positive multiple of 4 (dv=%d)", dv);
+  AILA_REQUIRE(B <= 65535, "deltanet_decode: B too large (%d)", B);
+  const dim3 grid(Hv, B, (dv + kColQuads * 4 - 1) / (kColQuads * 4));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16* qp = static_cast<const bf16*>(q);
+  const bf16* kp = static_cast<const bf16*>(k);
+  const bf16* vp = static_cast<const bf16*>(v);
+  const bf16* ap = static_cast<const bf16*>(a);
+  const bf16* bp = static_cast<const bf16*>(b);
+  const bf16* dtp = static_cast<const bf16*>(dt_bias);
+  bf16* op = static_cast<bf16*>(out);
+  switch (dk) {
+    case 64:
+      hipLaunchKernelGGL(deltanet_decode_kernel<64>, grid, dim3(kThreads), 0, st, qp, kp, vp, ap,
+                         bp, dtp, A_log, state, op, Hk, Hv, dv, eps, scale);
+      break;
+    case 128:
+      hipLaunchKernelGGL(deltanet_decode_kernel<128>, grid, dim3(kThreads), 0, st, qp, kp, vp, ap,
+                         bp, dtp, A_log, state, op, Hk, Hv, dv, eps, scale);
+      break;
+    case 256:
+      hipLaunchKernelGGL(deltanet_decode_kernel<256>, grid, dim3(kThreads), 0, st, qp, kp, vp, ap,
+                         bp, dtp, A_log, state, op, Hk, Hv, dv, eps, scale);
+      break;
+    default:
+      return set_error(AILA_HIP_EUNSUPPORTED, "deltanet_decode: dk=%d not in {64,128,256}", dk);
+  }
+  return check_launch("deltanet_decode");
+}

@@ -1,0 +1,354 @@
+// Split-K flash-decode for single-token GQA over a bf16 KV cache (gfx950).
+//
+// Reference: ops::attention_decode (src/ops/AttentionOps.cpp:499-643) with
+// its baseline kernel (:73-166) and the exact split/merge kernel for D=256
+// (:168-320). One design serves every (D, group) here:
+//
+//  * Grid (split, kv_head, sequence). A workgroup (4 waves) owns a range of
+//    `split_len` cache rows of one KV head and ALL G = Hq/Hkv query heads of
+//    that group, so each K/V byte is read from HBM once per step.
+//  * Scores on MFMA: v_mfma_f32_16x16x32_bf16 with A = the G query heads
+//    (rows, zero padded to 16) and B = 16 cache rows. Lane l loads 16 bytes of
+//    row (t0 + l%16) at byte offset 64*ks + 16*(l/16): each load instruction
+//    reads 16 rows x 64 contiguous bytes, and lanes 0..15 receive the scores
+//    of heads 0..3 for 16 tokens.
+//  * Online softmax in the log2 domain; per-head block maxima are reduced
+//    with DPP row operations inside the 16-lane row that holds the head.
+//  * P.V on VALU: P goes through a small per-wave LDS slice; V rows are read
+//    with coalesced 16-byte loads (D/8 lanes per row) and accumulated into
+//    per-lane fp32 registers.
+//  * Waves of a workgroup merge through LDS; a workgroup writes either the
+//    final bf16 output (one split) or a partial record {m, l, acc[D]} in the
+//    reference's layout (AttentionOps.cpp:50-51: [0]=m, [1]=l, [16..]=acc,
+//    m in natural-log units), merged by gqa_decode_merge_kernel (:276-319).
+#include "common.hpp"
+
+namespace aila {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTokPerWaveIter = 32;   // two MFMA column groups of 16 tokens
+constexpr int kMaxSplits = 256;
+constexpr int kRecHeader = 16;
+
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ kc,
+    const bf16* __restrict__ vc, bf16* __restrict__ out,
+    float* __restrict__ part, int Hq, int Hkv, int max_seq, int L,
+    const int* __restrict__ seq_lens, int split_len, int nsplit_max,
+    float scale_log2) {
+  static_assert(D % 32 == 0 && D <= 256, "D");
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "G");
+  constexpr int KS = D / 32;          // MFMA k-steps over the head dim
+  constexpr int VL = D / 8;           // lanes per V row (16 B each)
+  constexpr int VR = 64 / VL;         // V rows per load instruction
+  constexpr int GR = (G + 3) / 4;     // 16-lane rows holding score heads
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  int len = L;
+  if (seq_lens) len = min(max(seq_lens[b], 0), L);
+  const int s0 = split * split_len;
+  const int nsplit_b = (len + split_len - 1) / split_len;
+  const bool single = (part == nullptr);
+  if (!single && split >= nsplit_b) return;   // the merge reads nsplit_b records
+  const int s1 = min(s0 + split_len, len);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m16 = lane & 15, g4 = lane >> 4;
+  const size_t kv_off = (static_cast<size_t>(b) * Hkv + kvh) * max_seq * D;
+  const bf16* K = kc + kv_off;
+  const bf16* V = vc + kv_off;
+  const int h0 = kvh * G;             // first query head of the group
+
+  __shared__ float s_p[kWaves][kTokPerWaveIter][G];
+  __shared__ float s_acc[kWaves][G][D];
+  __shared__ float s_ml[kWaves][2][G];
+
+  // Query operand (A rows = heads, zero rows for m16 >= G).
+  bf16x8_t qa[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (m16 < G) raw = ld16(q + (static_cast<size_t>(b) * Hq + h0 + m16) * D + ks * 32 + g4 * 8);
+    qa[ks] = as_bf16x8(raw);
+  }
+
+  float m_run[G], l_part[G], acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m_run[h] = -INFINITY;
+    l_part[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  }
+  const int vd = (lane % VL) * 8;
+  const int vr = lane / VL;
+
+  for (int t0 = s0 + wave * kTokPerWaveIter; t0 < s1; t0 += kWaves * kTokPerWaveIter) {
+    // ---- scores: two 16-token column groups --------------------------
+    f32x4 sc[2];
+#pragma unroll
+    for (int grp = 0; grp < 2; ++grp) {
+      const int tok = min(t0 + grp * 16 + m16, s1 - 1);   // clamp: always a valid row
+      const bf16* krow = K + static_cast<size_t>(tok) * D + g4 * 8;
+      u32x4 kb[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kb[ks] = ld16(krow + ks * 32);
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32(qa[ks], as_bf16x8(kb[ks]), c);
+      const bool valid = (t0 + grp * 16 + m16) < s1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[grp][j] = valid ? c[j] * scale_log2 : -INFINITY;
+    }
+    // ---- online softmax (log2 domain) ---------------------------------
+    float alpha[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const int j = h & 3, row = h >> 2;
+      float bm = row16_max(fmaxf(sc[0][j], sc[1][j]));
+      bm = readlane_f(bm, row * 16);
+      const float mn = fmaxf(m_run[h], bm);
+      alpha[h] = (m_run[h] == -INFINITY) ? 0.f : fast_exp2(m_run[h] - mn);
+      m_run[h] = mn;
+      l_part[h] *= alpha[h];
+    }
+    // p for the heads held by this lane's row; write to the wave's P slice.
+#pragma unroll
+    for (int r = 0; r < GR; ++r) {
+      if (g4 == r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int h = r * 4 + j;
+          if (h < G) {
+            const float mref = (m_run[h] == -INFINITY) ? 0.f : m_run[h];
+#pragma unroll
+            for (int grp = 0; grp < 2; ++grp) {
+              const float p = fast_exp2(sc[grp][j] - mref);
+              l_part[h] += p;
+              s_p[wave][grp * 16 + m16][h] = p;
+            }
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- P.V -----------------------------------------------------------
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
+    }
+#pragma unroll 4
+    for (int i = vr; i < kTokPerWaveIter; i += VR) {
+      const int tok = min(t0 + i, s1 - 1);
+      float vf[8];
+      unpack8(ld16(V + static_cast<size_t>(tok) * D + vd), vf);
+      float p[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) p[h] = s_p[wave][i][h];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] += p[h] * vf[e];
+      }
+    }
+    // The next iteration overwrites this wave's P slice.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- wave epilogue --------------------------------------------------
+  // l: per-lane partial sums live in the 16-lane row that owns the head.
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const int row = h >> 2;
+    float l = row16_sum(l_part[h]);
+    l = readlane_f(l, row * 16);
+    l_part[h] = l;
+  }
+  // Sum acc over the VR row phases (lanes with equal vd).
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = acc[h][e];
+#pragma unroll
+      for (int off = VL; off < 64; off <<= 1) x += __shfl_xor(x, off);
+      acc[h][e] = x;
+    }
+  }
+  if (vr == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[wave][h][vd + e] = acc[h][e];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      s_ml[wave][0][h] = m_run[h];
+      s_ml[wave][1][h] = l_part[h];
+    }
+  }
+  __syncthreads();
+
+  // ---- workgroup merge ------------------------------------------------
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int h = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0][h]);
+    float A = 0.f, Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = s_ml[w][0][h];
+      const float f = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+      A += f * s_acc[w][h][d];
+      Ls += f * s_ml[w][1][h];
+    }
+    const int hq = h0 + h;
+    if (single) {
+      out[(static_cast<size_t>(b) * Hq + hq) * D + d] = f2bf(Ls > 0.f ? A / Ls : 0.f);
+    } else {
+      float* rec = part + ((static_cast<size_t>(b) * Hq + hq) * nsplit_max + split) * (kRecHeader + D);
+      rec[kRecHeader + d] = A;
+      if (d == 0) {
+        rec[0] = (M == -INFINITY) ? -INFINITY : M * (1.0f / kLog2e);
+        rec[1] = Ls;
+      }
+    }
+  }
+}
+
+// Merge of split records, AttentionOps.cpp:276-319: M = max m_i,
+// out = sum_i e^(m_i - M) acc_i / sum_i e^(m_i - M) l_i.
+template <int D>
+__global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
+    const float* __restrict__ part, bf16* __restrict__ out, int Hq, int L,
+    const int* __restrict__ seq_lens, int split_len, int nsplit_max) {
+  const int hq = blockIdx.x, b = blockIdx.y;
+  int len = L;
+  if (seq_lens) len = min(max(seq_lens[b], 0), L);
+  const int ns = (len + split_len - 1) / split_len;
+  const float* rec0 = part + (static_cast<size_t>(b) * Hq + hq) * nsplit_max * (kRecHeader + D);
+  __shared__ float s_f[kMaxSplits];
+  __shared__ float s_inv;
+  // One wave computes the split factors.
+  if (threadIdx.x < 64) {
+    float M = -INFINITY;
+    for (int i = threadIdx.x; i < ns; i += 64) M = fmaxf(M, rec0[static_cast<size_t>(i) * (kRecHeader + D)]);
+    M = fmaxf(M, __shfl_xor(M, 32));
+    M = fmaxf(M, __shfl_xor(M, 16));
+    M = row16_max(M);
+    float Ls = 0.f;
+    for (int i = threadIdx.x; i < ns; i += 64) {
+      const float* r = rec0 + static_cast<size_t>(i) * (kRecHeader + D);
+      const float f = (r[0] == -INFINITY) ? 0.f : expf(r[0] - M);
+      s_f[i] = f;
+      Ls += f * r[1];
+    }
+    Ls = wave_sum(Ls);
+    if (threadIdx.x == 0) s_inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+  }
+  __syncthreads();
+  const float inv = s_inv;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float A = 0.f;
+    for (int i = 0; i < ns; ++i) A += s_f[i] * rec0[static_cast<size_t>(i) * (kRecHeader + D) + kRecHeader + d];
+    out[(static_cast<size_t>(b) * Hq + hq) * D + d] = f2bf(A * inv);
+  }
+}
+
+template <int D, int G>
+int launch_decode(const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
+                  float* part, int B, int Hq, int Hkv, int max_seq, int L,
+                  const int* seq_lens, int split_len, int nsplit,
+                  hipStream_t st) {
+  const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+  hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(nsplit, Hkv, B), dim3(kThreads), 0, st,
+                     q, kc, vc, out, part, Hq, Hkv, max_seq, L, seq_lens, split_len, kMaxSplits,
+                     scale_log2);
+  if (part) {
+    hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(Hq, B), dim3(256), 0, st, part, out, Hq,
+                       L, seq_lens, split_len, kMaxSplits);
+  }
+  return check_launch("gqa_decode");
+}
+
+template <int D>
+int dispatch_g(int G, const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
+               float* part, int B, int Hq, int Hkv, int max_seq, int L,
+               const int* seq_lens, int split_len, int nsplit, hipStream_t st) {
+  switch (G) {
+    case 1: return launch_decode<D, 1>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
+    case 2: return launch_decode<D, 2>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
+    case 4: return launch_decode<D, 4>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
+    case 8: return launch_decode<D, 8>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
+    default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: Hq/Hkv=%d not in {1,2,4,8}", G);
+  }
+}
+
+}  // namespace
+}  // namespace aila
+
+extern "C" size_t aila_hip_gqa_decode_workspace_size(int B, int Hq, int D) {
+  if (B <= 0 || Hq <= 0 || D <= 0) return 0;
+  return static_cast<size_t>(B) * Hq * aila::kMaxSplits * (aila::kRecHeader + D) * sizeof(float);
+}
+
+extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache,
+                                   const void* v_cache, void* out,
+                                   void* workspace, size_t workspace_bytes,
+                                   int B, int Hq, int Hkv, int D, int max_seq,
+                                   int cached_len, const int* seq_lens,
+                                   void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
+  AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
+               "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
+  AILA_REQUIRE(cached_len >= 0 && cached_len <= max_seq,
+               "gqa_decode: cached_len=%d outside [0, max_seq=%d]", cached_len, max_seq);
+  const int G = Hq / Hkv;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  bf16* o = static_cast<bf16*>(out);
+  float* part = nullptr;
+  int split_len, nsplit;
+  if (cached_len == 0) {
+    // Nothing to attend: the single-pass kernel writes a zero output.
+    split_len = 1;
+    nsplit = 1;
+  } else if (workspace) {
+    if (workspace_bytes < aila_hip_gqa_decode_workspace_size(B, Hq, D))
+      return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu < %zu bytes", workspace_bytes,
+                       aila_hip_gqa_decode_workspace_size(B, Hq, D));
+    // Aim for ~2048 workgroups (8 per CU on 256 CUs); splits are multiples
+    // of 128 rows (one pass of the four waves) and at most kMaxSplits.
+    const int groups = B * Hkv;
+    int want = (2048 + groups - 1) / groups;
+    want = max(1, min(want, kMaxSplits));
+    split_len = (cached_len + want - 1) / want;
+    split_len = ((split_len + 127) / 128) * 128;
+    nsplit = (cached_len + split_len - 1) / split_len;
+    if (nsplit == 1) part = nullptr;   // one split: write the output directly
+    else part = static_cast<float*>(workspace);
+  } else {
+    split_len = cached_len;
+    nsplit = 1;
+  }
+  const bf16* qp = static_cast<const bf16*>(q);
+  const bf16* kp = static_cast<const bf16*>(k_cache);
+  const bf16* vp = static_cast<const bf16*>(v_cache);
+  switch (D) {
+    case 64: return dispatch_g<64>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, st);
+    case 128: return dispatch_g<128>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, st);
+    case 256: return dispatch_g<256>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, st);
+    default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: D=%d not in {64,128,256}", D);
+  }
+}

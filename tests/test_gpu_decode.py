@@ -1,0 +1,169 @@
+"""GPU parity: GQA split-K decode and DeltaNet decode vs the CPU oracle.
+
+Tolerances (from the path's contract): bf16 attention outputs within max
+relative error 1e-2 of the fp32 oracle; the DeltaNet fp32 state within 1e-3
+relative after 2048 steps.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from aila_amd import datagen as dg
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 1e-2
+STATE_TOL = 1e-3
+
+
+def _t(x, dtype=None):
+    import torch
+    if x.dtype == np.uint16:
+        return torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _np_bf16(t):
+    return t.detach().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+
+def _relerr(a, r):
+    return float(np.max(np.abs(a - r)) / max(float(np.max(np.abs(r))), 1e-30))
+
+
+def _decode_case(seed, B, Hq, Hkv, D, max_seq, L, split=True, seq_lens=None, poison=True):
+    import torch
+    import aila_amd
+    q = dg.normal_bf16(seed, 0, (B, Hq, D))
+    kc = dg.normal_bf16(seed, 1, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 2, (B, Hkv, max_seq, D))
+    if poison and max_seq > L:
+        kc[:, :, L:] = 0x7FC0   # NaN: any read past cached_len poisons the output
+        vc[:, :, L:] = 0x7FC0
+    ws = None
+    if split:
+        ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    sl = None
+    if seq_lens is not None:
+        sl = torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
+    out = aila_amd.gqa_decode(_t(q), _t(kc), _t(vc), L, workspace=ws, seq_lens=sl)
+    torch.cuda.synchronize()
+    got = dg.bf16_to_f32(_np_bf16(out))
+    lens = seq_lens if seq_lens is not None else [L] * B
+    for b in range(B):
+        lb = min(lens[b], L)
+        if lb == 0:
+            assert not got[b].any()
+            continue
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(
+            q[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv, D, max_seq, lb))[0]
+        err = _relerr(got[b], want)
+        assert np.isfinite(got[b]).all(), f"non-finite output b={b}"
+        assert err <= ATTN_TOL, f"b={b} L={lb} relerr={err}"
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_decode_config1_qwen3_0p6b(split):
+    # B=1, 16 q heads, 8 kv heads, D=128, context 512.
+    _decode_case(0xA11A, 1, 16, 8, 128, 520, 512, split=split)
+
+
+@pytest.mark.parametrize("D,G", [(64, 1), (64, 8), (128, 2), (128, 4), (256, 4), (256, 8), (256, 2)])
+def test_decode_shapes(D, G):
+    Hkv = 2
+    _decode_case(1000 + D + G, 2, Hkv * G, Hkv, D, 1100, 1037, split=True)
+
+
+@pytest.mark.parametrize("L", [1, 15, 16, 17, 127, 128, 129, 4095])
+def test_decode_lengths(L):
+    _decode_case(2000 + L, 1, 16, 4, 256, L + 33, L, split=True)
+
+
+def test_decode_per_sequence_lengths_and_empty():
+    _decode_case(3001, 4, 8, 2, 128, 800, 777, split=True, seq_lens=[777, 0, 1, 300])
+    _decode_case(3002, 4, 8, 2, 128, 800, 777, split=False, seq_lens=[5, 777, 0, 64])
+
+
+def test_decode_zero_length():
+    _decode_case(3003, 2, 8, 2, 128, 64, 0, split=True)
+
+
+def test_decode_long_context_qwen35_shape():
+    # One layer of BASELINE config 5 at reduced batch: 16q/4kv, D=256, 32k.
+    _decode_case(3004, 1, 16, 4, 256, 32768 + 8, 32768, split=True, poison=True)
+
+
+def test_decode_rejects_bad_shapes():
+    import torch
+    import aila_amd
+    q = torch.zeros((1, 12, 128), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, 4, 64, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(aila_amd.AilaHipError):
+        aila_amd.gqa_decode(q, kc, kc, 10)          # G = 3 unsupported
+    q = torch.zeros((1, 8, 96), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, 4, 64, 96), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(aila_amd.AilaHipError):
+        aila_amd.gqa_decode(q, kc, kc, 10)          # D = 96 unsupported
+    q = torch.zeros((1, 8, 128), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, 4, 64, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(aila_amd.AilaHipError):
+        aila_amd.gqa_decode(q, kc, kc, 65)          # cached_len > max_seq
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(aila_amd.AilaHipError):
+        aila_amd.gqa_decode(q, kc, kc, 60, workspace=ws)
+
+
+# ------------------------------------------------------------ DeltaNet ----
+def _dn_inputs(seed, B, T, Hk, Hv, dk, dv):
+    q = dg.normal_bf16(seed, 0, (B, T, Hk, dk))
+    k = dg.normal_bf16(seed, 1, (B, T, Hk, dk))
+    v = dg.normal_bf16(seed, 2, (B, T, Hv, dv))
+    a = dg.normal_bf16(seed, 3, (B, T, Hv))
+    b = dg.normal_bf16(seed, 4, (B, T, Hv))
+    S0 = dg.normal(seed, 5, B * Hv * dk * dv, std=0.02).reshape(B, Hv, dk, dv)
+    return q, k, v, a, b, S0
+
+
+def _run_dn_steps(q, k, v, a, b, S0, dt_bias=None, A_log=None):
+    import torch
+    import aila_amd
+    B, T = q.shape[:2]
+    dq, dk_, dv_, da, db = (_t(np.ascontiguousarray(x)) for x in (q, k, v, a, b))
+    st = _t(S0.astype(np.float32))
+    dtb = _t(dt_bias) if dt_bias is not None else None
+    alog = _t(A_log) if A_log is not None else None
+    outs = []
+    for t in range(T):
+        o = aila_amd.deltanet_decode(dq[:, t].contiguous(), dk_[:, t].contiguous(),
+                                     dv_[:, t].contiguous(), da[:, t].contiguous(),
+                                     db[:, t].contiguous(), st, dt_bias=dtb, A_log=alog)
+        outs.append(o)
+    torch.cuda.synchronize()
+    out = torch.stack(outs, dim=1)
+    return _np_bf16(out), st.cpu().numpy()
+
+
+@pytest.mark.parametrize("Hk,Hv,dk,dv", [(4, 4, 128, 128), (2, 4, 128, 128), (2, 2, 64, 64),
+                                          (1, 2, 256, 128), (2, 2, 128, 200)])
+def test_deltanet_decode_short(Hk, Hv, dk, dv):
+    B, T = 3, 16
+    q, k, v, a, b, S0 = _dn_inputs(4000 + dk + dv + Hv, B, T, Hk, Hv, dk, dv)
+    dtb = dg.normal_bf16(4000, 6, (Hv,), std=0.5)
+    alog = dg.normal(4000, 7, Hv, std=0.3)
+    got_o, got_S = _run_dn_steps(q, k, v, a, b, S0, dtb, alog)
+    _, want_ob, want_S = oracle.deltanet_recurrent(q, k, v, a, b, S0, B, T, Hk, Hv, dk, dv,
+                                                   dt_bias=dtb, A_log=alog)
+    assert _relerr(got_S, want_S) <= STATE_TOL
+    assert _relerr(dg.bf16_to_f32(got_o), dg.bf16_to_f32(want_ob)) <= ATTN_TOL
+
+
+def test_deltanet_decode_2048_steps_state_tolerance():
+    # BASELINE config 3 statistics (N(0,0.02) state, L2-normed q/k, sigmoid
+    # beta, alpha = exp(-softplus(a))) with B=4, H=16 to keep the oracle fast.
+    B, T, H, d = 4, 2048, 16, 128
+    q, k, v, a, b, S0 = _dn_inputs(0xA11A + 2, B, T, H, H, d, d)
+    got_o, got_S = _run_dn_steps(q, k, v, a, b, S0)
+    _, want_ob, want_S = oracle.deltanet_recurrent(q, k, v, a, b, S0, B, T, H, H, d, d)
+    err = _relerr(got_S, want_S)
+    assert err <= STATE_TOL, err
+    assert _relerr(dg.bf16_to_f32(got_o[:, -1]), dg.bf16_to_f32(want_ob[:, -1])) <= ATTN_TOL
