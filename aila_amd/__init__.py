@@ -27,6 +27,9 @@ _SIGS = {
     "aila_hip_version": ([], _I),
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_gqa_prefill": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "aila_hip_gqa_prefill_cached": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "aila_hip_copy_to_cache": ([_P, _P, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _F, _F, _P], _I),
 }
@@ -122,6 +125,62 @@ def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
                                    int(cached_len), _ptr(seq_lens), _stream(stream))
     _check(rc, "aila_hip_gqa_decode")
     return out
+
+
+def gqa_prefill(q, k, v, Hq: int, Hkv: int, out=None, k_cache=None, v_cache=None,
+                cache_pos: int = 0, stream=None):
+    """Causal prefill. q [S, Hq*D], k/v [S, Hkv*D] bf16 -> out [S, Hq*D].
+    With k_cache/v_cache [Hkv, max_seq, D], k/v are also written to cache
+    rows [cache_pos, cache_pos + S)."""
+    import torch
+    S = q.shape[0]
+    D = q.shape[1] // Hq
+    _need(q, torch.bfloat16, (S, Hq * D), "q")
+    _need(k, torch.bfloat16, (S, Hkv * D), "k")
+    _need(v, torch.bfloat16, (S, Hkv * D), "v")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.bfloat16, (S, Hq * D), "out")
+    max_seq = 0
+    if k_cache is not None or v_cache is not None:
+        max_seq = k_cache.shape[1]
+        _need(k_cache, torch.bfloat16, (Hkv, max_seq, D), "k_cache")
+        _need(v_cache, torch.bfloat16, (Hkv, max_seq, D), "v_cache")
+    rc = lib().aila_hip_gqa_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(k_cache),
+                                    _ptr(v_cache), int(cache_pos), max_seq, S, Hq, Hkv, D,
+                                    _stream(stream))
+    _check(rc, "aila_hip_gqa_prefill")
+    return out
+
+
+def gqa_prefill_cached(q, k_cache, v_cache, start_pos: int, Hq: int, out=None, stream=None):
+    """q [S, Hq*D] at positions start_pos.. attends cache [Hkv, max_seq, D]."""
+    import torch
+    S = q.shape[0]
+    Hkv, max_seq, D = k_cache.shape
+    _need(q, torch.bfloat16, (S, Hq * D), "q")
+    _need(k_cache, torch.bfloat16, (Hkv, max_seq, D), "k_cache")
+    _need(v_cache, torch.bfloat16, (Hkv, max_seq, D), "v_cache")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.bfloat16, (S, Hq * D), "out")
+    rc = lib().aila_hip_gqa_prefill_cached(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), S,
+                                           int(start_pos), Hq, Hkv, D, max_seq, _stream(stream))
+    _check(rc, "aila_hip_gqa_prefill_cached")
+    return out
+
+
+def copy_to_cache(new_kv, cache, start_pos: int, stream=None):
+    """new_kv [S, H*D] bf16 -> cache [H, max_seq, D] rows [start_pos, start_pos+S)."""
+    import torch
+    H, max_seq, D = cache.shape
+    S = new_kv.shape[0]
+    _need(new_kv, torch.bfloat16, (S, H * D), "new_kv")
+    _need(cache, torch.bfloat16, (H, max_seq, D), "cache")
+    rc = lib().aila_hip_copy_to_cache(_ptr(new_kv), _ptr(cache), S, int(start_pos), H, D, max_seq,
+                                      _stream(stream))
+    _check(rc, "aila_hip_copy_to_cache")
+    return cache
 
 
 # ------------------------------------------------------------ DeltaNet ----

@@ -62,6 +62,38 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int B, int Hq, int Hkv, int D, int max_seq,
                         int cached_len, const int* seq_lens, void* stream);
 
+/* Causal GQA prefill over the current chunk on bf16 MFMA (flash attention).
+ * Replaces ops::attention_prefill (src/ops/Ops.hpp:278-282;
+ * src/ops/AttentionOps.cpp:649-842) fused with the two ops::copy_to_cache
+ * calls that precede it in the backends (Ops.hpp:199-201,
+ * AttentionOps.cpp:2513-2532; Qwen3DenseBackend.cpp:320-327).
+ *   q [S, Hq*D], k/v [S, Hkv*D] bf16 (token-major, already QK-normed/RoPE'd)
+ *   out [S, Hq*D] bf16; query i attends keys [0, i].
+ *   k_cache/v_cache [Hkv, max_seq, D] bf16 or both NULL: when given, k/v are
+ *   also written to cache rows [cache_pos, cache_pos + S).
+ * Supported: D in {64, 128, 256}, Hq % Hkv == 0. */
+int aila_hip_gqa_prefill(const void* q, const void* k, const void* v, void* out,
+                         void* k_cache, void* v_cache, int cache_pos,
+                         int max_seq, int S, int Hq, int Hkv, int D,
+                         void* stream);
+
+/* Incremental (cached) prefill: replaces ops::attention_prefill_cached
+ * (src/ops/Ops.hpp:293-298; src/ops/AttentionOps.cpp:2308-2507).
+ *   q [S, Hq*D]; k_cache/v_cache [Hkv, max_seq, D] already holding rows
+ *   [0, start_pos + S); query i (position start_pos + i) attends cache rows
+ *   [0, start_pos + i]. out [S, Hq*D] bf16. */
+int aila_hip_gqa_prefill_cached(const void* q, const void* k_cache,
+                                const void* v_cache, void* out, int S,
+                                int start_pos, int Hq, int Hkv, int D,
+                                int max_seq, void* stream);
+
+/* ops::copy_to_cache (src/ops/Ops.hpp:199-201; AttentionOps.cpp:2513-2532):
+ * new_kv [S, H*D] bf16 -> cache [H, max_seq, D] rows [start_pos, start_pos+S).
+ * Requires D % 8 == 0 and 16-byte aligned pointers. */
+int aila_hip_copy_to_cache(const void* new_kv, void* cache, int S,
+                           int start_pos, int H, int D, int max_seq,
+                           void* stream);
+
 /* ----------------------------------------------------------- DeltaNet --- */
 
 /* One Gated DeltaNet decode step (the recurrence of

@@ -1,0 +1,167 @@
+"""GPU parity: causal GQA prefill (MFMA flash attention), the cached
+(incremental) variant and copy_to_cache vs the CPU oracle.
+
+Tolerance: bf16 outputs within max relative error 1e-2 of the fp32 oracle.
+Cache writes are bit-exact copies.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from aila_amd import datagen as dg
+
+pytestmark = pytest.mark.gpu
+ATTN_TOL = 1e-2
+
+
+def _t(x):
+    import torch
+    if x.dtype == np.uint16:
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _np(t):
+    import torch
+    return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _relerr(a, r):
+    return float(np.max(np.abs(a - r)) / max(float(np.max(np.abs(r))), 1e-30))
+
+
+def qk_prepped(seed, S, Hq, Hkv, D, start_pos=0, theta=1e6):
+    """BASELINE config-2 inputs: N(0,1) bf16, QK RMS-norm, RoPE, bf16 after each."""
+    q = dg.normal_bf16(seed, 0, (S, Hq * D))
+    k = dg.normal_bf16(seed, 1, (S, Hkv * D))
+    v = dg.normal_bf16(seed, 2, (S, Hkv * D))
+    q = oracle.head_rms_norm(q, 1e-6, S, Hq, D)
+    k = oracle.head_rms_norm(k, 1e-6, S, Hkv, D)
+    q, k = oracle.apply_rope(q, k, S, start_pos, Hq, Hkv, D, D, theta)
+    return q, k, v
+
+
+def _prefill_case(seed, S, Hq, Hkv, D, with_cache=False, cache_pos=0, prepped=False):
+    import torch
+    import aila_amd
+    if prepped:
+        q, k, v = qk_prepped(seed, S, Hq, Hkv, D)
+    else:
+        q = dg.normal_bf16(seed, 0, (S, Hq * D))
+        k = dg.normal_bf16(seed, 1, (S, Hkv * D))
+        v = dg.normal_bf16(seed, 2, (S, Hkv * D))
+    kc = vc = None
+    if with_cache:
+        max_seq = cache_pos + S + 5
+        kc = torch.full((Hkv, max_seq, D), 7.0, dtype=torch.bfloat16, device="cuda")
+        vc = torch.full((Hkv, max_seq, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    out = aila_amd.gqa_prefill(_t(q), _t(k), _t(v), Hq, Hkv, k_cache=kc, v_cache=vc,
+                               cache_pos=cache_pos)
+    torch.cuda.synchronize()
+    got = dg.bf16_to_f32(_np(out))
+    want = dg.bf16_to_f32(oracle.attention_prefill_naive(q, k, v, S, Hq, Hkv, D))
+    assert np.isfinite(got).all()
+    err = _relerr(got, want)
+    assert err <= ATTN_TOL, f"S={S} Hq={Hq} Hkv={Hkv} D={D}: relerr {err}"
+    # per-row check guards against a single wrong row hiding under the max
+    rows = np.max(np.abs(got - want), axis=1) / np.maximum(np.max(np.abs(want), axis=1), 1e-30)
+    assert np.max(rows) <= 2 * ATTN_TOL
+    if with_cache:
+        max_seq = kc.shape[1]
+        ck = np.full((Hkv, max_seq, D), dg.f32_to_bf16(np.float32([7.0]))[0], np.uint16)
+        cv = ck.copy()
+        oracle.copy_to_cache(k, ck, S, cache_pos, Hkv, D, max_seq)
+        oracle.copy_to_cache(v, cv, S, cache_pos, Hkv, D, max_seq)
+        assert np.array_equal(_np(kc), ck)
+        assert np.array_equal(_np(vc), cv)
+    return err
+
+
+def test_prefill_config2_qwen3_4b():
+    # S=2048, 32 q heads, 8 kv heads, D=128, QK-norm, RoPE 1e6,
+    # causal; the KV cache is written for later decode.
+    _prefill_case(0xA11A + 1, 2048, 32, 8, 128, with_cache=True, prepped=True)
+
+
+@pytest.mark.parametrize("S", [1, 2, 17, 64, 127, 128, 129, 300])
+def test_prefill_ragged_lengths(S):
+    _prefill_case(5000 + S, S, 8, 2, 128)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 4, 4), (64, 8, 1), (256, 8, 2), (256, 16, 4), (128, 16, 16)])
+def test_prefill_shapes(D, Hq, Hkv):
+    _prefill_case(6000 + D + Hq, 333, Hq, Hkv, D, with_cache=True, cache_pos=3)
+
+
+def test_prefill_qwen35_full_attention_shape():
+    # Qwen3.5 full-attention layer: 16 q / 4 kv heads, D=256, S=1024
+    _prefill_case(6100, 1024, 16, 4, 256, prepped=True)
+
+
+@pytest.mark.parametrize("S,start,D", [(1, 100, 128), (37, 91, 128), (256, 1000, 128), (64, 64, 256),
+                                       (130, 7, 64)])
+def test_prefill_cached(S, start, D):
+    import torch
+    import aila_amd
+    Hq, Hkv = 8, 2
+    max_seq = start + S + 9
+    kc = dg.normal_bf16(7000 + S, 1, (Hkv, max_seq, D))
+    vc = dg.normal_bf16(7000 + S, 2, (Hkv, max_seq, D))
+    kc[:, start + S:] = 0x7FC0      # NaN poison beyond the attended rows
+    vc[:, start + S:] = 0x7FC0
+    q = dg.normal_bf16(7000 + S, 0, (S, Hq * D))
+    out = aila_amd.gqa_prefill_cached(_t(q), _t(kc), _t(vc), start, Hq)
+    torch.cuda.synchronize()
+    got = dg.bf16_to_f32(_np(out))
+    want = dg.bf16_to_f32(oracle.attention_prefill_cached(q, kc, vc, S, start, Hq, Hkv, D, max_seq))
+    assert np.isfinite(got).all()
+    assert _relerr(got, want) <= ATTN_TOL
+
+
+def test_copy_to_cache_bit_exact():
+    import torch
+    import aila_amd
+    S, H, D, start, max_seq = 50, 4, 128, 13, 80
+    src = dg.normal_bf16(7100, 0, (S, H * D))
+    cache = torch.zeros((H, max_seq, D), dtype=torch.bfloat16, device="cuda")
+    aila_amd.copy_to_cache(_t(src), cache, start)
+    torch.cuda.synchronize()
+    want = np.zeros((H, max_seq, D), np.uint16)
+    oracle.copy_to_cache(src, want, S, start, H, D, max_seq)
+    assert np.array_equal(_np(cache), want)
+
+
+def test_prefill_then_decode_uses_written_cache():
+    # prefill writes the cache; decode of one more token over it matches the oracle
+    import torch
+    import aila_amd
+    S, Hq, Hkv, D = 200, 16, 8, 128
+    max_seq = 256
+    q, k, v = qk_prepped(7200, S, Hq, Hkv, D)
+    kc = torch.zeros((1, Hkv, max_seq, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros((1, Hkv, max_seq, D), dtype=torch.bfloat16, device="cuda")
+    aila_amd.gqa_prefill(_t(q), _t(k), _t(v), Hq, Hkv, k_cache=kc[0], v_cache=vc[0])
+    qd = dg.normal_bf16(7201, 0, (1, Hq, D))
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(1, Hq, D), dtype=torch.uint8, device="cuda")
+    out = aila_amd.gqa_decode(_t(qd), kc, vc, S, workspace=ws)
+    torch.cuda.synchronize()
+    ck = np.zeros((1, Hkv, max_seq, D), np.uint16)
+    cv = np.zeros((1, Hkv, max_seq, D), np.uint16)
+    oracle.copy_to_cache(k, ck[0], S, 0, Hkv, D, max_seq)
+    oracle.copy_to_cache(v, cv[0], S, 0, Hkv, D, max_seq)
+    want = dg.bf16_to_f32(oracle.attention_decode_baseline(qd, ck, cv, 1, Hq, Hkv, D, max_seq, S))
+    assert _relerr(dg.bf16_to_f32(_np(out)), want) <= ATTN_TOL
+
+
+def test_prefill_rejects_bad_args():
+    import torch
+    import aila_amd
+    q = torch.zeros((16, 8 * 96), dtype=torch.bfloat16, device="cuda")
+    kv = torch.zeros((16, 2 * 96), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(aila_amd.AilaHipError):
+        aila_amd.gqa_prefill(q, kv, kv, 8, 2)       # D=96
+    q = torch.zeros((16, 8 * 128), dtype=torch.bfloat16, device="cuda")
+    kv = torch.zeros((16, 2 * 128), dtype=torch.bfloat16, device="cuda")
+    cache = torch.zeros((2, 20, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(aila_amd.AilaHipError):
+        aila_amd.gqa_prefill(q, kv, kv, 8, 2, k_cache=cache, v_cache=cache, cache_pos=10)
