@@ -32,6 +32,9 @@ _SIGS = {
     "aila_hip_copy_to_cache": ([_P, _P, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _F, _F, _P], _I),
+    "aila_hip_deltanet_prefill_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "aila_hip_deltanet_prefill": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ,
+                                   _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
 }
 
 
@@ -212,4 +215,43 @@ def deltanet_decode(q, k, v, a, b, state, out=None, dt_bias=None, A_log=None,
                                         B, Hk, Hv, dk, dv, float(eps), float(scale),
                                         _stream(stream))
     _check(rc, "aila_hip_deltanet_decode")
+    return out
+
+
+def deltanet_prefill_workspace_size(B: int, T: int, Hv: int, dk: int, dv: int) -> int:
+    return int(lib().aila_hip_deltanet_prefill_workspace_size(B, T, Hv, dk, dv))
+
+
+def deltanet_prefill(q, k, v, a, b, state, out=None, workspace=None, dt_bias=None,
+                     A_log=None, eps: float = 1e-6, scale: float | None = None, stream=None):
+    """Chunked prefill over T tokens. q,k [B,T,Hk,dk]; v [B,T,Hv,dv]; a,b
+    [B,T,Hv] bf16; state [B,Hv,dk,dv] fp32 (in/out) -> out [B,T,Hv,dv] bf16.
+    ``workspace``: uint8 device tensor (allocated here when None)."""
+    import torch
+    B, T, Hk, dk = q.shape
+    Hv, dv = v.shape[2], v.shape[3]
+    _need(q, torch.bfloat16, (B, T, Hk, dk), "q")
+    _need(k, torch.bfloat16, (B, T, Hk, dk), "k")
+    _need(v, torch.bfloat16, (B, T, Hv, dv), "v")
+    _need(a, torch.bfloat16, (B, T, Hv), "a", align=2)
+    _need(b, torch.bfloat16, (B, T, Hv), "b", align=2)
+    _need(state, torch.float32, (B, Hv, dk, dv), "state")
+    if dt_bias is not None:
+        _need(dt_bias, torch.bfloat16, (Hv,), "dt_bias", align=2)
+    if A_log is not None:
+        _need(A_log, torch.float32, (Hv,), "A_log", align=4)
+    if out is None:
+        out = torch.empty((B, T, Hv, dv), dtype=torch.bfloat16, device=q.device)
+    _need(out, torch.bfloat16, (B, T, Hv, dv), "out")
+    need = deltanet_prefill_workspace_size(B, T, Hv, dk, dv)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size()
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    rc = lib().aila_hip_deltanet_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b),
+                                         _ptr(dt_bias), _ptr(A_log), _ptr(state), _ptr(out),
+                                         _ptr(workspace), ws_bytes, B, T, Hk, Hv, dk, dv,
+                                         float(eps), float(scale), _stream(stream))
+    _check(rc, "aila_hip_deltanet_prefill")
     return out

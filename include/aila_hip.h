@@ -116,6 +116,29 @@ int aila_hip_deltanet_decode(const void* q, const void* k, const void* v,
                              int dk, int dv, float eps, float scale,
                              void* stream);
 
+/* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W, U, P, K^T and
+ * decay factors; about 72.8 KiB per (sequence, value head, 64-token chunk)).
+ * 0 for unsupported shapes. */
+size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk,
+                                                int dv);
+
+/* Chunked Gated DeltaNet prefill (chunk 64, WY/UT form on bf16 MFMA): the
+ * recurrence of aila_hip_deltanet_decode applied to T tokens, replacing the
+ * token-sequential Qwen35HybridTextBackend::run_linear_delta_prefill_gpu_batched
+ * (src/models/Qwen35HybridTextBackend.cpp:1306-1508) after conv1d/SiLU.
+ *   q, k [B, T, Hk, dk] bf16; v [B, T, Hv, dv] bf16; a, b [B, T, Hv] bf16
+ *   dt_bias [Hv] bf16 / A_log [Hv] fp32 may be NULL
+ *   state [B, Hv, dk, dv] fp32: initial state in, final state out
+ *   out [B, T, Hv, dv] bf16
+ * Supported: dk = dv = 128. */
+int aila_hip_deltanet_prefill(const void* q, const void* k, const void* v,
+                              const void* a, const void* b,
+                              const void* dt_bias, const float* A_log,
+                              float* state, void* out, void* workspace,
+                              size_t workspace_bytes, int B, int T, int Hk,
+                              int Hv, int dk, int dv, float eps, float scale,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif
