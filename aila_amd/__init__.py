@@ -27,6 +27,7 @@ _SIGS = {
     "aila_hip_version": ([], _I),
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_kv_append": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_prefill": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_gqa_prefill_cached": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_copy_to_cache": ([_P, _P, _I, _I, _I, _I, _I, _P], _I),
@@ -128,6 +129,21 @@ def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
                                    int(cached_len), _ptr(seq_lens), _stream(stream))
     _check(rc, "aila_hip_gqa_decode")
     return out
+
+
+def kv_append(k_new, v_new, k_cache, v_cache, pos: int = 0, positions=None, stream=None):
+    """k_new/v_new [B,Hkv,D] -> cache [B,Hkv,max_seq,D] row pos (or positions[b])."""
+    import torch
+    B, Hkv, max_seq, D = k_cache.shape
+    _need(k_new, torch.bfloat16, (B, Hkv, D), "k_new")
+    _need(v_new, torch.bfloat16, (B, Hkv, D), "v_new")
+    _need(k_cache, torch.bfloat16, (B, Hkv, max_seq, D), "k_cache")
+    _need(v_cache, torch.bfloat16, (B, Hkv, max_seq, D), "v_cache")
+    if positions is not None:
+        _need(positions, torch.int32, (B,), "positions", align=4)
+    rc = lib().aila_hip_kv_append(_ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), B, Hkv, D,
+                                  max_seq, int(pos), _ptr(positions), _stream(stream))
+    _check(rc, "aila_hip_kv_append")
 
 
 def gqa_prefill(q, k, v, Hq: int, Hkv: int, out=None, k_cache=None, v_cache=None,

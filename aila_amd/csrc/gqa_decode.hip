@@ -352,3 +352,40 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache,
     default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: D=%d not in {64,128,256}", D);
   }
 }
+
+namespace aila {
+namespace {
+// One new token per sequence: k_new/v_new [B, Hkv, D] -> cache row pos
+// (or positions[b]) of [B, Hkv, max_seq, D]. One 16-byte chunk per thread.
+__global__ void kv_append_kernel(const u32x4* __restrict__ kn, const u32x4* __restrict__ vn,
+                                 bf16* __restrict__ kc, bf16* __restrict__ vc, int B, int Hkv,
+                                 int D, int max_seq, int pos, const int* __restrict__ positions) {
+  const int chunks = D / 8;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * Hkv * chunks) return;
+  const int b = i / (Hkv * chunks);
+  const int h = (i / chunks) % Hkv;
+  const int c = i % chunks;
+  const int p = positions ? positions[b] : pos;
+  if (p < 0 || p >= max_seq) return;
+  const size_t dst = ((static_cast<size_t>(b) * Hkv + h) * max_seq + p) * D + c * 8;
+  *reinterpret_cast<u32x4*>(kc + dst) = kn[i];
+  *reinterpret_cast<u32x4*>(vc + dst) = vn[i];
+}
+}  // namespace
+}  // namespace aila
+
+extern "C" int aila_hip_kv_append(const void* k_new, const void* v_new, void* k_cache,
+                                  void* v_cache, int B, int Hkv, int D, int max_seq, int pos,
+                                  const int* positions, void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(k_new && v_new && k_cache && v_cache, "kv_append: null pointer");
+  AILA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D % 8 == 0, "kv_append: bad shape (B=%d Hkv=%d D=%d)", B, Hkv, D);
+  AILA_REQUIRE(positions || (pos >= 0 && pos < max_seq), "kv_append: pos=%d outside [0, max_seq=%d)", pos, max_seq);
+  const int n = B * Hkv * (D / 8);
+  hipLaunchKernelGGL(kv_append_kernel, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(k_new), static_cast<const u32x4*>(v_new),
+                     static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache), B, Hkv, D, max_seq, pos,
+                     positions);
+  return check_launch("kv_append");
+}

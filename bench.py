@@ -1,0 +1,465 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline workload: decode of a Qwen3.5-4B-shaped hybrid
+attention stack, 32 layers in a 3:1 pattern (24 Gated DeltaNet layers with
+16 qk / 32 v heads, dk = dv = 128, fp32 state; 8 GQA layers with 16 q / 4 kv
+heads, head_dim 256, bf16 KV cache), batch 8, context 32768, one new token
+per step. A step is one token through all 32 layers: for each GQA layer the
+new K/V row is appended and split-K decode runs over the cache; for each
+DeltaNet layer the state is updated once. value = algorithmic HBM bytes per
+step / step time (GB/s). Steps are replayed from HIP graphs (device-side
+lengths advance inside the graph), so host launch overhead is not timed.
+
+Also reported (sub-metrics, same run): GQA prefill TFLOP/s (config 2),
+DeltaNet decode us/step (config 3), DeltaNet chunked prefill tok/s
+(config 4), GQA decode latency at config 1, the roofline of the dominant
+kernel (GQA split-K decode, HIP events around each launch) and a CPU
+baseline (the scalar oracle on the host cores, bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "GQA decode HBM GB/s @32k ctx; prefill MFMA TFLOP/s; DeltaNet tok/s (1 GPU)"
+
+# config 5 shape
+B5, L5 = 8, 32768
+GQA_HQ, GQA_HKV, GQA_D = 16, 4, 256
+DN_HK, DN_HV, DN_D = 16, 32, 128
+N_LAYERS, N_GQA = 32, 8
+NPOOL = 4   # distinct activation sets (one captured graph each)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gqa_bytes(B, Hq, Hkv, D, L):
+    """Algorithmic bytes of one GQA decode launch: K and V rows read once,
+    q read and out written once."""
+    return 2 * B * Hkv * L * D * 2 + 2 * B * Hq * D * 2
+
+
+def deltanet_bytes(B, Hk, Hv, dk, dv):
+    """State read + write once, q,k,v,a,b read, out written."""
+    return (2 * B * Hv * dk * dv * 4 + 2 * B * Hk * dk * 2 + B * Hv * dv * 2
+            + 2 * B * Hv * 2 + B * Hv * dv * 2)
+
+
+def time_graph(torch, g, reps):
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps  # ms
+
+
+# ------------------------------------------------------------- config 5 ----
+def build_config5(torch, aila_amd, steps, warmup):
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xA11A + 4)
+    max_seq = L5 + warmup + steps + 8
+    kc, vc = [], []
+    for _ in range(N_GQA):
+        k = torch.empty((B5, GQA_HKV, max_seq, GQA_D), dtype=torch.bfloat16, device=dev)
+        v = torch.empty_like(k)
+        k.normal_(generator=gen)
+        v.normal_(generator=gen)
+        kc.append(k)
+        vc.append(v)
+    states = [torch.empty((B5, DN_HV, DN_D, DN_D), dtype=torch.float32, device=dev).normal_(0, 0.02, generator=gen)
+              for _ in range(N_LAYERS - N_GQA)]
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    pool = []
+    for _ in range(NPOOL):
+        layers = []
+        for layer in range(N_LAYERS):
+            if layer % 4 == 3:
+                layers.append(dict(q=torch.randn((B5, GQA_HQ, GQA_D), generator=gen, **bf),
+                                   k=torch.randn((B5, GQA_HKV, GQA_D), generator=gen, **bf),
+                                   v=torch.randn((B5, GQA_HKV, GQA_D), generator=gen, **bf)))
+            else:
+                layers.append(dict(q=torch.randn((B5, DN_HK, DN_D), generator=gen, **bf),
+                                   k=torch.randn((B5, DN_HK, DN_D), generator=gen, **bf),
+                                   v=torch.randn((B5, DN_HV, DN_D), generator=gen, **bf),
+                                   a=torch.randn((B5, DN_HV), generator=gen, **bf),
+                                   b=torch.randn((B5, DN_HV), generator=gen, **bf)))
+        pool.append(layers)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B5, GQA_HQ, GQA_D), dtype=torch.uint8, device=dev)
+    gqa_out = torch.empty((B5, GQA_HQ, GQA_D), **bf)
+    dn_out = torch.empty((B5, DN_HV, DN_D), **bf)
+    # device-side lengths: positions = row written this step, lens = rows attended
+    positions = torch.full((B5,), L5, dtype=torch.int32, device=dev)
+    lens = torch.full((B5,), L5 + 1, dtype=torch.int32, device=dev)
+    return dict(kc=kc, vc=vc, states=states, pool=pool, ws=ws, gqa_out=gqa_out, dn_out=dn_out,
+                positions=positions, lens=lens, max_seq=max_seq)
+
+
+def step5(aila_amd, W, p):
+    """One decode token through the 32-layer stack (activation set p)."""
+    gi = di = 0
+    for layer in range(N_LAYERS):
+        x = W["pool"][p][layer]
+        if layer % 4 == 3:
+            aila_amd.kv_append(x["k"], x["v"], W["kc"][gi], W["vc"][gi], positions=W["positions"])
+            aila_amd.gqa_decode(x["q"], W["kc"][gi], W["vc"][gi], W["max_seq"], out=W["gqa_out"],
+                                workspace=W["ws"], seq_lens=W["lens"])
+            gi += 1
+        else:
+            aila_amd.deltanet_decode(x["q"], x["k"], x["v"], x["a"], x["b"], W["states"][di],
+                                     out=W["dn_out"])
+            di += 1
+    W["positions"].add_(1)
+    W["lens"].add_(1)
+
+
+def bench_config5(torch, aila_amd, steps, warmup):
+    W = build_config5(torch, aila_amd, steps, warmup)
+    graphs = []
+    # capture NPOOL graphs, one per activation set; capture does not execute,
+    # so lengths are unchanged by it.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step5(aila_amd, W, 0)     # warm the launch path once (eager)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    W["positions"].fill_(L5)
+    W["lens"].fill_(L5 + 1)
+    for p in range(NPOOL):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step5(aila_amd, W, p)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs[i % NPOOL].replay()
+    torch.cuda.synchronize()
+    L_first = int(W["lens"][0].item())
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s.record()
+    for i in range(steps):
+        graphs[(warmup + i) % NPOOL].replay()
+    e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = s.elapsed_time(e) / steps
+    # algorithmic bytes per step, averaged over the timed lengths
+    L_mean = L_first + (steps - 1) / 2.0
+    gqa_b = gqa_bytes(B5, GQA_HQ, GQA_HKV, GQA_D, L_mean) + 2 * B5 * GQA_HKV * GQA_D * 2 * 2
+    dn_b = deltanet_bytes(B5, DN_HK, DN_HV, DN_D, DN_D)
+    step_bytes = N_GQA * gqa_b + (N_LAYERS - N_GQA) * dn_b
+    return dict(ms=ms, wall=wall, step_bytes=step_bytes, gqa_step_bytes=N_GQA * gqa_b,
+                dn_step_bytes=(N_LAYERS - N_GQA) * dn_b, L_first=L_first, W=W)
+
+
+def roofline_gqa(torch, aila_amd, W, reps=64):
+    """Dominant kernel: one GQA decode launch (split + merge dispatch) on a
+    config-5 layer at L = 32768, HIP events around each launch on the stream
+    the kernels run on (torch's current stream)."""
+    L = L5
+    lens = torch.full((B5,), L, dtype=torch.int32, device="cuda")
+    x = W["pool"][0][3]
+    fn = lambda: aila_amd.gqa_decode(x["q"], W["kc"][0], W["vc"][0], L, out=W["gqa_out"],
+                                     workspace=W["ws"], seq_lens=lens)
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for s, e in evs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    durs = [s.elapsed_time(e) for s, e in evs]
+    avg_ms = statistics.mean(durs)
+    byts = gqa_bytes(B5, GQA_HQ, GQA_HKV, GQA_D, L)
+    achieved = byts / (avg_ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gqa_decode_config5_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    return {"kernel": "gqa_decode_split_kernel<256,4> + merge", "bound": "hbm",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes": byts, "avg_launch_us": round(avg_ms * 1e3, 2)}
+
+
+def profile_kernel(torch, aila_amd, reps=20):
+    """Dominant kernel alone (one config-5 GQA layer, B=8, L=32768) plus a
+    plain 1 GiB device-to-device copy used to calibrate the HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE) against a known traffic."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0xA11A + 4)
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    kc = torch.empty((B5, GQA_HKV, L5, GQA_D), **bf).normal_(generator=g)
+    vc = torch.empty_like(kc).normal_(generator=g)
+    q = torch.randn((B5, GQA_HQ, GQA_D), generator=g, **bf)
+    out = torch.empty_like(q)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B5, GQA_HQ, GQA_D), dtype=torch.uint8, device=dev)
+    src = torch.empty(1 << 29, **bf).normal_(generator=g)   # 1 GiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        aila_amd.gqa_decode(q, kc, vc, L5, out=out, workspace=ws)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[profile] gqa_decode x{reps} (algorithmic {gqa_bytes(B5, GQA_HQ, GQA_HKV, GQA_D, L5)} B/launch), "
+        f"copy x{reps} ({2 * src.numel() * 2} B/launch: 1 GiB read + 1 GiB write)")
+
+
+# ------------------------------------------------------------ sub-metrics --
+def sub_prefill(torch, aila_amd, reps=20):
+    S, Hq, Hkv, D = 2048, 32, 8, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 1)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    q = torch.randn((S, Hq * D), generator=g, **bf)
+    k = torch.randn((S, Hkv * D), generator=g, **bf)
+    v = torch.randn((S, Hkv * D), generator=g, **bf)
+    out = torch.empty_like(q)
+    kc = torch.empty((Hkv, S, D), **bf)
+    vc = torch.empty_like(kc)
+    fn = lambda: aila_amd.gqa_prefill(q, k, v, Hq, Hkv, out=out, k_cache=kc, v_cache=vc)
+    for _ in range(3):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) / reps * 1e3
+    flops = 4 * D * Hq * S * (S + 1) / 2
+    return {"config": "2: S=2048 Hq=32 Hkv=8 D=128 causal + cache write", "us": round(us, 2),
+            "tflops": round(flops / us / 1e6, 1), "frac_of_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+
+
+def sub_deltanet_decode(torch, aila_amd, steps=2048, per_graph=16):
+    B, H, d = 32, 16, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 2)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    st = torch.empty((B, H, d, d), dtype=torch.float32, device="cuda").normal_(0, 0.02, generator=g)
+    xs = [dict(q=torch.randn((B, H, d), generator=g, **bf), k=torch.randn((B, H, d), generator=g, **bf),
+               v=torch.randn((B, H, d), generator=g, **bf), a=torch.randn((B, H), generator=g, **bf),
+               b=torch.randn((B, H), generator=g, **bf)) for _ in range(per_graph)]
+    out = torch.empty((B, H, d), **bf)
+    for x in xs:
+        aila_amd.deltanet_decode(x["q"], x["k"], x["v"], x["a"], x["b"], st, out=out)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for x in xs:
+            aila_amd.deltanet_decode(x["q"], x["k"], x["v"], x["a"], x["b"], st, out=out)
+    gr.replay()
+    ms = time_graph(torch, gr, steps // per_graph)
+    us = ms * 1e3 / per_graph
+    byts = deltanet_bytes(B, H, H, d, d)
+    bound_us = byts / (HBM_PEAK_GBS * 1e3)
+    return {"config": "3: B=32 H=16 dk=dv=128, 2048 sequential steps", "us_per_step": round(us, 3),
+            "GBps": round(byts / us / 1e3, 1), "x_of_state_traffic_bound": round(us / bound_us, 3)}
+
+
+def sub_deltanet_prefill(torch, aila_amd, reps=10):
+    B, T, Hk, Hv, d = 1, 4096, 16, 32, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 3)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    q = torch.randn((B, T, Hk, d), generator=g, **bf)
+    k = torch.randn((B, T, Hk, d), generator=g, **bf)
+    v = torch.randn((B, T, Hv, d), generator=g, **bf)
+    a = torch.randn((B, T, Hv), generator=g, **bf)
+    b = torch.randn((B, T, Hv), generator=g, **bf)
+    st = torch.zeros((B, Hv, d, d), dtype=torch.float32, device="cuda")
+    out = torch.empty((B, T, Hv, d), **bf)
+    ws = torch.empty(aila_amd.deltanet_prefill_workspace_size(B, T, Hv, d, d), dtype=torch.uint8, device="cuda")
+    fn = lambda: aila_amd.deltanet_prefill(q, k, v, a, b, st, out=out, workspace=ws)
+    fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) / reps * 1e3
+    byts = 103.8e6
+    flops = 23.98e9
+    frac = max(byts / (HBM_PEAK_GBS * 1e9), flops / (BF16_PEAK_TFLOPS * 1e12)) / (us * 1e-6)
+    return {"config": "4: T=4096 C=64 Hk=16 Hv=32 dk=dv=128", "us": round(us, 1),
+            "tok_per_s": round(T / (us * 1e-6)), "roofline_frac": round(frac, 4)}
+
+
+def sub_decode_cfg1(torch, aila_amd, per_graph=32, reps=20):
+    B, Hq, Hkv, D, L = 1, 16, 8, 128, 512
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    q = torch.randn((B, Hq, D), generator=g, **bf)
+    kc = torch.randn((B, Hkv, L, D), generator=g, **bf)
+    vc = torch.randn((B, Hkv, L, D), generator=g, **bf)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    aila_amd.gqa_decode(q, kc, vc, L, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for _ in range(per_graph):
+            aila_amd.gqa_decode(q, kc, vc, L, out=out, workspace=ws)
+    gr.replay()
+    us = time_graph(torch, gr, reps) * 1e3 / per_graph
+    byts = gqa_bytes(B, Hq, Hkv, D, L)
+    return {"config": "1: B=1 Hq=16 Hkv=8 D=128 L=512", "us_per_call": round(us, 2),
+            "GBps": round(byts / us / 1e3, 1)}
+
+
+# ------------------------------------------------------------ CPU baseline --
+def cpu_baseline(min_seconds=10.0):
+    """The scalar oracle (fast-math build, OpenMP over heads) on the host
+    cores: one 3:1 layer group of config 5 (3 DeltaNet layers + 1 GQA layer
+    with the reference's split-K tile 128), batch 1, L = 32768, repeated
+    until ~min_seconds of CPU work; GB/s of the same algorithmic bytes."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(0xA11A + 4)
+
+    def bf16(shape):
+        x = rng.standard_normal(int(np.prod(shape)), dtype=np.float32)
+        return (x.view(np.uint32) >> 16).astype(np.uint16).reshape(shape)
+
+    L = L5
+    q = bf16((1, GQA_HQ, GQA_D))
+    kc = bf16((1, GQA_HKV, L, GQA_D))
+    vc = bf16((1, GQA_HKV, L, GQA_D))
+    dn = [dict(q=bf16((1, 1, DN_HK, DN_D)), k=bf16((1, 1, DN_HK, DN_D)), v=bf16((1, 1, DN_HV, DN_D)),
+               a=bf16((1, 1, DN_HV)), b=bf16((1, 1, DN_HV)),
+               S=(rng.standard_normal((1, DN_HV, DN_D, DN_D), dtype=np.float32) * 0.02)) for _ in range(3)]
+    lib = oracle.lib(fast=True)
+    threads = oracle.num_threads(fast=True)
+
+    def one():
+        oracle.attention_decode_splitk(q, kc, vc, 1, GQA_HQ, GQA_HKV, GQA_D, L, L, 128, fast=True)
+        for x in dn:
+            oracle.deltanet_recurrent(x["q"], x["k"], x["v"], x["a"], x["b"], x["S"], 1, 1, DN_HK,
+                                      DN_HV, DN_D, DN_D, fast=True)
+
+    one()
+    times = []
+    t_end = time.perf_counter() + min_seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    byts = gqa_bytes(1, GQA_HQ, GQA_HKV, GQA_D, L) + 3 * deltanet_bytes(1, DN_HK, DN_HV, DN_D, DN_D)
+    del lib
+    return {"value": round(byts / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle/liboracle_fast.so (-O3 -ffast-math, OpenMP {threads} threads): one config-5 "
+                       f"layer group (1 GQA layer split-K tile 128 + 3 DeltaNet layers), batch 1, L={L}; "
+                       f"median of {len(times)} runs ({sum(times):.1f} s)"),
+            "seconds_per_group": round(t, 4)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-sub", action="store_true", help="skip the config 1-4 sub-metrics")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only run the dominant kernel (config-5 GQA decode layer, L=32768) and a "
+                         "1 GiB device copy, 20 times each, for rocprofv3 counter runs")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path "
+              "has no multi-GPU mode in this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import aila_amd
+    aila_amd.lib()   # fail loudly if the HIP library is missing
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+
+    if args.profile_kernel:
+        profile_kernel(torch, aila_amd)
+        return
+    log(f"[bench] config 5: {args.warmup} warmup + {args.steps} timed steps")
+    r5 = bench_config5(torch, aila_amd, args.steps, args.warmup)
+    value = r5["step_bytes"] / (r5["ms"] * 1e-3) / 1e9
+    log(f"[bench] config 5: {r5['ms']:.3f} ms/step, {value:.0f} GB/s")
+    roof = roofline_gqa(torch, aila_amd, r5["W"])
+    log(f"[bench] roofline gqa_decode: {roof['achieved']} GB/s ({roof['frac']*100:.1f}%)")
+    del r5["W"]
+    torch.cuda.empty_cache()
+    sub = {}
+    if not args.no_sub:
+        sub["gqa_prefill"] = sub_prefill(torch, aila_amd)
+        log(f"[bench] prefill {sub['gqa_prefill']}")
+        sub["deltanet_decode"] = sub_deltanet_decode(torch, aila_amd)
+        log(f"[bench] deltanet decode {sub['deltanet_decode']}")
+        sub["deltanet_prefill"] = sub_deltanet_prefill(torch, aila_amd)
+        log(f"[bench] deltanet prefill {sub['deltanet_prefill']}")
+        sub["gqa_decode_cfg1"] = sub_decode_cfg1(torch, aila_amd)
+        log(f"[bench] decode cfg1 {sub['gqa_decode_cfg1']}")
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline ...")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"[bench] CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r5["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("config 5: Qwen3.5-4B-shaped hybrid attention stack decode, 24 Gated DeltaNet "
+                         "(16qk/32v heads, dk=dv=128, fp32 state) + 8 GQA (16q/4kv, D=256, bf16 KV) layers"),
+            "batch": B5, "context": r5["L_first"], "layers": N_LAYERS,
+            "step_bytes": int(r5["step_bytes"]), "gqa_step_bytes": int(r5["gqa_step_bytes"]),
+            "deltanet_step_bytes": int(r5["dn_step_bytes"]), "parallelism": "single GPU",
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "sub": sub,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -62,6 +62,16 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int B, int Hq, int Hkv, int D, int max_seq,
                         int cached_len, const int* seq_lens, void* stream);
 
+/* Append one decoded token's K and V per sequence to the cache (the
+ * cache-write half of ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:
+ * 105-216, without the norm/RoPE): k_new/v_new [B, Hkv, D] bf16 ->
+ * k_cache/v_cache [B, Hkv, max_seq, D] row `pos`, or row positions[b] when
+ * the optional device int[B] `positions` is given (rows outside
+ * [0, max_seq) are skipped). Requires D % 8 == 0. */
+int aila_hip_kv_append(const void* k_new, const void* v_new, void* k_cache,
+                       void* v_cache, int B, int Hkv, int D, int max_seq,
+                       int pos, const int* positions, void* stream);
+
 /* Causal GQA prefill over the current chunk on bf16 MFMA (flash attention).
  * Replaces ops::attention_prefill (src/ops/Ops.hpp:278-282;
  * src/ops/AttentionOps.cpp:649-842) fused with the two ops::copy_to_cache

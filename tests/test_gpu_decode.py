@@ -167,3 +167,25 @@ def test_deltanet_decode_2048_steps_state_tolerance():
     err = _relerr(got_S, want_S)
     assert err <= STATE_TOL, err
     assert _relerr(dg.bf16_to_f32(got_o[:, -1]), dg.bf16_to_f32(want_ob[:, -1])) <= ATTN_TOL
+
+
+def test_kv_append_bit_exact():
+    import torch
+    import aila_amd
+    B, Hkv, max_seq, D = 3, 4, 40, 256
+    kc = torch.zeros((B, Hkv, max_seq, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kn = dg.normal_bf16(4100, 0, (B, Hkv, D))
+    vn = dg.normal_bf16(4100, 1, (B, Hkv, D))
+    aila_amd.kv_append(_t(kn), _t(vn), kc, vc, pos=17)
+    pos = torch.tensor([0, 39, 5], dtype=torch.int32, device="cuda")
+    aila_amd.kv_append(_t(vn), _t(kn), kc, vc, positions=pos)
+    torch.cuda.synchronize()
+    k_np, v_np = _np_bf16(kc), _np_bf16(vc)
+    assert np.array_equal(k_np[:, :, 17], kn) and np.array_equal(v_np[:, :, 17], vn)
+    for b, p in enumerate([0, 39, 5]):
+        assert np.array_equal(k_np[b, :, p], vn[b]) and np.array_equal(v_np[b, :, p], kn[b])
+    touched = {17, 0, 39, 5}
+    for p in range(max_seq):
+        if p not in touched:
+            assert not k_np[:, :, p].any()
