@@ -21,6 +21,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libaila_hip.so")
+OPS_LIB = os.path.join(HERE, "libaila_ops.so")
+HOST = os.path.join(HERE, "host")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -53,8 +55,15 @@ def build(verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # C++ ops:: layer over the C ABI (host code only)
+    host_srcs = sorted(glob.glob(os.path.join(HOST, "*.cpp")))
+    cmd = [HIPCC, "-std=c++17", "-O2", "-fPIC", "-shared", "-I", HOST, "-I", os.path.join(ROOT, "include"),
+           *host_srcs, "-o", OPS_LIB, "-L", HERE, "-laila_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"ops layer build failed:\n{r.stderr}")
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources and {OPS_LIB}")
     return LIB
 
 

@@ -23,6 +23,8 @@
 //    m in natural-log units), merged by gqa_decode_merge_kernel (:276-319).
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace aila {
 namespace {
 
@@ -269,15 +271,15 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
 template <int D, int G>
 int launch_decode(const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
                   float* part, int B, int Hq, int Hkv, int max_seq, int L,
-                  const int* seq_lens, int split_len, int nsplit,
+                  const int* seq_lens, int split_len, int nsplit, int nsplit_max,
                   hipStream_t st) {
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
   hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(nsplit, Hkv, B), dim3(kThreads), 0, st,
-                     q, kc, vc, out, part, Hq, Hkv, max_seq, L, seq_lens, split_len, kMaxSplits,
+                     q, kc, vc, out, part, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit_max,
                      scale_log2);
   if (part) {
     hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(Hq, B), dim3(256), 0, st, part, out, Hq,
-                       L, seq_lens, split_len, kMaxSplits);
+                       L, seq_lens, split_len, nsplit_max);
   }
   return check_launch("gqa_decode");
 }
@@ -285,12 +287,12 @@ int launch_decode(const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
 template <int D>
 int dispatch_g(int G, const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
                float* part, int B, int Hq, int Hkv, int max_seq, int L,
-               const int* seq_lens, int split_len, int nsplit, hipStream_t st) {
+               const int* seq_lens, int split_len, int nsplit, int nsplit_max, hipStream_t st) {
   switch (G) {
-    case 1: return launch_decode<D, 1>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
-    case 2: return launch_decode<D, 2>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
-    case 4: return launch_decode<D, 4>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
-    case 8: return launch_decode<D, 8>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, st);
+    case 1: return launch_decode<D, 1>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
+    case 2: return launch_decode<D, 2>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
+    case 4: return launch_decode<D, 4>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
+    case 8: return launch_decode<D, 8>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
     default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: Hq/Hkv=%d not in {1,2,4,8}", G);
   }
 }
@@ -320,19 +322,24 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache,
   bf16* o = static_cast<bf16*>(out);
   float* part = nullptr;
   int split_len, nsplit;
+  // Records per (sequence, head) that the workspace holds; the split count
+  // adapts to it (the reference's [Hq, max_tiles, 272] partials buffer for
+  // D=256 is accepted as-is).
+  const size_t rec_bytes = static_cast<size_t>(B) * Hq * (kRecHeader + D) * sizeof(float);
+  const int nsplit_max = workspace ? static_cast<int>(std::min<size_t>(workspace_bytes / rec_bytes, kMaxSplits)) : 0;
+  if (workspace && nsplit_max < 2)
+    return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu bytes holds < 2 split records (%zu bytes each)",
+                     workspace_bytes, rec_bytes);
   if (cached_len == 0) {
     // Nothing to attend: the single-pass kernel writes a zero output.
     split_len = 1;
     nsplit = 1;
   } else if (workspace) {
-    if (workspace_bytes < aila_hip_gqa_decode_workspace_size(B, Hq, D))
-      return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu < %zu bytes", workspace_bytes,
-                       aila_hip_gqa_decode_workspace_size(B, Hq, D));
     // Aim for ~2048 workgroups (8 per CU on 256 CUs); splits are multiples
-    // of 128 rows (one pass of the four waves) and at most kMaxSplits.
+    // of 128 rows (one pass of the four waves).
     const int groups = B * Hkv;
     int want = (2048 + groups - 1) / groups;
-    want = max(1, min(want, kMaxSplits));
+    want = max(1, min(want, nsplit_max));
     split_len = (cached_len + want - 1) / want;
     split_len = ((split_len + 127) / 128) * 128;
     nsplit = (cached_len + split_len - 1) / split_len;
@@ -346,9 +353,9 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache,
   const bf16* kp = static_cast<const bf16*>(k_cache);
   const bf16* vp = static_cast<const bf16*>(v_cache);
   switch (D) {
-    case 64: return dispatch_g<64>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, st);
-    case 128: return dispatch_g<128>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, st);
-    case 256: return dispatch_g<256>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, st);
+    case 64: return dispatch_g<64>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, nsplit_max, st);
+    case 128: return dispatch_g<128>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, nsplit_max, st);
+    case 256: return dispatch_g<256>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, nsplit_max, st);
     default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: D=%d not in {64,128,256}", D);
   }
 }

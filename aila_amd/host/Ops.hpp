@@ -1,0 +1,74 @@
+// ops:: attention hot path on MI355X: the reference's operator interface
+// (Aila src/ops/Ops.hpp:196-298) with the same names, argument order and
+// meaning, implemented over the C ABI in include/aila_hip.h. Every op
+// enqueues on ctx.stream() and returns before completion; failures of the
+// underlying C ABI (bad shapes, unsupported head_dim, launch errors) are
+// thrown as std::runtime_error.
+#pragma once
+
+#include "Context.hpp"
+#include "Tensor.hpp"
+
+namespace aila {
+namespace ops {
+
+// new_kv [seq_len, num_heads*head_dim] -> cache [num_heads, max_seq_len,
+// head_dim] at start_pos (Ops.hpp:196-201).
+void copy_to_cache(Context& ctx, Tensor& new_kv, Tensor& cache, int seq_len, int start_pos,
+                   int num_heads, int head_dim, int max_seq_len);
+
+// Single-token GQA decode (Ops.hpp:259-269). q [1, Hq*D]; k_cache/v_cache
+// [Hkv, max_seq, D] (max_seq read from k_cache.shape(1), as the reference
+// does at AttentionOps.cpp:87); output [1, Hq*D]. scores_buf is accepted and
+// unused. exact_partials_buf (fp32, e.g. the backend's [Hq, max_tiles, 272]
+// buffer) enables split-K with as many splits as it holds records; null runs
+// the single-pass kernel.
+void attention_decode(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output,
+                      Tensor& scores_buf, int num_heads, int num_kv_heads, int head_dim,
+                      int cached_len, Tensor* exact_partials_buf = nullptr);
+
+// Causal prefill over the current chunk (Ops.hpp:271-282). q [S, Hq*D],
+// k/v [S, Hkv*D]; output [S, Hq*D]. scores_buf is accepted and unused (no
+// [H, S, S] score matrix is materialised).
+void attention_prefill(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& output,
+                       Tensor& scores_buf, int seq_len, int num_heads, int num_kv_heads,
+                       int head_dim);
+
+// attention_prefill fused with the two copy_to_cache calls that precede it in
+// the backends (Qwen3DenseBackend.cpp:320-327): k/v are also written to the
+// caches at start_pos. Addition; the reference issues three ops.
+void attention_prefill_write_cache(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& output,
+                                   Tensor& k_cache, Tensor& v_cache, int seq_len, int start_pos,
+                                   int num_heads, int num_kv_heads, int head_dim, int max_seq_len);
+
+// Incremental prefill against the cache (Ops.hpp:284-298).
+void attention_prefill_cached(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache,
+                              Tensor& output, Tensor& scores_buf, int seq_len, int start_pos,
+                              int num_heads, int num_kv_heads, int head_dim, int max_seq_len);
+
+// Gated DeltaNet recurrence, one token (the state update of
+// Qwen35HybridTextBackend::run_linear_delta_decode_gpu,
+// Qwen35HybridTextBackend.cpp:975-1166, after conv1d/SiLU and before the
+// gated RMSNorm). q,k [Hk*dk] bf16, v [Hv*dv] bf16, a,b [Hv] bf16 (one
+// sequence; batch via the leading dim of state [B, Hv, dk, dv] fp32),
+// out [Hv*dv] bf16 = scale * S^T q. dt_bias (bf16 [Hv]) and A_log (fp32 [Hv])
+// may be null.
+void linear_delta_decode(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& a, Tensor& b,
+                         Tensor* dt_bias, Tensor* A_log, Tensor& state, Tensor& out,
+                         int num_k_heads, int num_v_heads, int head_k_dim, int head_v_dim,
+                         float eps, float scale);
+
+// Chunked prefill of the same recurrence over seq_len tokens (replaces the
+// token-sequential run_linear_delta_prefill_gpu_batched,
+// Qwen35HybridTextBackend.cpp:1306-1508). q,k [S, Hk*dk]; v [S, Hv*dv];
+// a,b [S, Hv]; out [S, Hv*dv]; workspace u8 of at least
+// linear_delta_prefill_workspace_bytes(...).
+size_t linear_delta_prefill_workspace_bytes(int seq_len, int num_v_heads, int head_k_dim,
+                                            int head_v_dim);
+void linear_delta_prefill(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& a, Tensor& b,
+                          Tensor* dt_bias, Tensor* A_log, Tensor& state, Tensor& out,
+                          Tensor& workspace, int seq_len, int num_k_heads, int num_v_heads,
+                          int head_k_dim, int head_v_dim, float eps, float scale);
+
+}  // namespace ops
+}  // namespace aila

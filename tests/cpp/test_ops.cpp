@@ -1,0 +1,191 @@
+// C++ parity test of the ops:: layer (aila_amd/host) on the GPU, checked
+// against the CPU oracle (oracle/liboracle.so). Exit code 0 = all passed.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#include "Ops.hpp"
+
+extern "C" {
+void orc_attention_decode_baseline(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
+                                   int, int, int, int);
+void orc_attention_prefill_naive(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
+                                 int, int);
+void orc_attention_prefill_cached(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
+                                  int, int, int, int, int);
+void orc_copy_to_cache(const uint16_t*, uint16_t*, int, int, int, int, int);
+void orc_deltanet_recurrent(const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,
+                            const uint16_t*, const uint16_t*, const float*, float*, float*, uint16_t*, int,
+                            int, int, int, int, int, float, float, int);
+uint16_t orc_f32_to_bf16(float);
+float orc_bf16_to_f32(uint16_t);
+}
+
+using namespace aila;
+using u16v = std::vector<uint16_t>;
+
+static int g_fail = 0;
+
+static uint64_t g_state = 0x1234567ull;
+static float nrand() {  // Box-Muller over a 64-bit LCG (test-local inputs)
+  auto u = [] {
+    g_state = g_state * 6364136223846793005ull + 1442695040888963407ull;
+    return ((g_state >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+  };
+  return static_cast<float>(std::sqrt(-2.0 * std::log(u())) * std::cos(6.283185307179586 * u()));
+}
+static u16v rand_bf16(size_t n) {
+  u16v v(n);
+  for (auto& x : v) x = orc_f32_to_bf16(nrand());
+  return v;
+}
+static double relerr(const u16v& a, const u16v& r) {
+  double m = 0, d = 0;
+  for (size_t i = 0; i < a.size(); ++i) {
+    const double x = orc_bf16_to_f32(a[i]), y = orc_bf16_to_f32(r[i]);
+    d = std::fmax(d, std::fabs(x - y));
+    m = std::fmax(m, std::fabs(y));
+  }
+  return d / std::fmax(m, 1e-30);
+}
+static double relerr_f(const std::vector<float>& a, const std::vector<float>& r) {
+  double m = 0, d = 0;
+  for (size_t i = 0; i < a.size(); ++i) {
+    d = std::fmax(d, std::fabs(a[i] - r[i]));
+    m = std::fmax(m, std::fabs(r[i]));
+  }
+  return d / std::fmax(m, 1e-30);
+}
+static void expect(bool ok, const char* name, double err) {
+  std::printf("%-44s %s (err %.3g)\n", name, ok ? "OK" : "FAIL", err);
+  if (!ok) ++g_fail;
+}
+template <typename T>
+static Tensor upload(Context& ctx, const std::vector<T>& h, std::vector<int64_t> shape, DType dt) {
+  Tensor t = Tensor::allocate(ctx, shape, dt);
+  ctx.memcpy_h2d(t.data(), h.data(), h.size() * sizeof(T));
+  return t;
+}
+template <typename T>
+static std::vector<T> download(Context& ctx, Tensor& t) {
+  std::vector<T> h(t.numel());
+  ctx.memcpy_d2h(h.data(), t.data(), h.size() * sizeof(T));
+  return h;
+}
+
+int main() {
+  Context ctx;
+  // ---- attention_decode with the reference backend's partials buffer ----
+  {
+    const int Hq = 16, Hkv = 4, D = 256, max_seq = 4096, L = 3001;
+    const int max_tiles = (max_seq + 127) / 128;
+    u16v q = rand_bf16(Hq * D), kc = rand_bf16(size_t(Hkv) * max_seq * D), vc = rand_bf16(size_t(Hkv) * max_seq * D);
+    Tensor tq = upload(ctx, q, {1, Hq * D}, DType::bf16), tk = upload(ctx, kc, {Hkv, max_seq, D}, DType::bf16),
+           tv = upload(ctx, vc, {Hkv, max_seq, D}, DType::bf16);
+    Tensor out = Tensor::allocate(ctx, {1, Hq * D});
+    Tensor scores = Tensor::allocate(ctx, {Hq, max_seq}, DType::f32);
+    Tensor partials = Tensor::allocate(ctx, {Hq, max_tiles, 272}, DType::f32);
+    u16v want(Hq * D);
+    orc_attention_decode_baseline(q.data(), kc.data(), vc.data(), want.data(), 1, Hq, Hkv, D, max_seq, L);
+    ops::attention_decode(ctx, tq, tk, tv, out, scores, Hq, Hkv, D, L, &partials);
+    double e = relerr(download<uint16_t>(ctx, out), want);
+    expect(e <= 1e-2, "attention_decode (split-K, backend partials)", e);
+    ops::attention_decode(ctx, tq, tk, tv, out, scores, Hq, Hkv, D, L, nullptr);
+    e = relerr(download<uint16_t>(ctx, out), want);
+    expect(e <= 1e-2, "attention_decode (single pass)", e);
+  }
+  // ---- prefill + copy_to_cache, fused variant, cached prefill -------------
+  {
+    const int S = 300, Hq = 32, Hkv = 8, D = 128, max_seq = 512, start = 100, S2 = 64;
+    u16v q = rand_bf16(size_t(S) * Hq * D), k = rand_bf16(size_t(S) * Hkv * D), v = rand_bf16(size_t(S) * Hkv * D);
+    Tensor tq = upload(ctx, q, {S, Hq * D}, DType::bf16), tk = upload(ctx, k, {S, Hkv * D}, DType::bf16),
+           tv = upload(ctx, v, {S, Hkv * D}, DType::bf16);
+    Tensor out = Tensor::allocate(ctx, {S, Hq * D}), scores = Tensor::allocate(ctx, {1}, DType::f32);
+    Tensor kc = Tensor::allocate(ctx, {Hkv, max_seq, D}), vc = Tensor::allocate(ctx, {Hkv, max_seq, D});
+    u16v want(size_t(S) * Hq * D);
+    orc_attention_prefill_naive(q.data(), k.data(), v.data(), want.data(), S, Hq, Hkv, D);
+    ops::copy_to_cache(ctx, tk, kc, S, start, Hkv, D, max_seq);
+    ops::copy_to_cache(ctx, tv, vc, S, start, Hkv, D, max_seq);
+    ops::attention_prefill(ctx, tq, tk, tv, out, scores, S, Hq, Hkv, D);
+    double e = relerr(download<uint16_t>(ctx, out), want);
+    expect(e <= 1e-2, "attention_prefill", e);
+    u16v ck(size_t(Hkv) * max_seq * D, 0), cv(size_t(Hkv) * max_seq * D, 0);
+    u16v got_k = download<uint16_t>(ctx, kc), got_v = download<uint16_t>(ctx, vc);
+    orc_copy_to_cache(k.data(), ck.data(), S, start, Hkv, D, max_seq);
+    orc_copy_to_cache(v.data(), cv.data(), S, start, Hkv, D, max_seq);
+    bool same = true;
+    for (int h = 0; h < Hkv; ++h)
+      for (int r = start; r < start + S; ++r)
+        same &= !std::memcmp(&got_k[(size_t(h) * max_seq + r) * D], &ck[(size_t(h) * max_seq + r) * D], D * 2) &&
+                !std::memcmp(&got_v[(size_t(h) * max_seq + r) * D], &cv[(size_t(h) * max_seq + r) * D], D * 2);
+    expect(same, "copy_to_cache (bit exact)", same ? 0 : 1);
+    Tensor kc2 = Tensor::allocate(ctx, {Hkv, max_seq, D}), vc2 = Tensor::allocate(ctx, {Hkv, max_seq, D});
+    ops::attention_prefill_write_cache(ctx, tq, tk, tv, out, kc2, vc2, S, start, Hq, Hkv, D, max_seq);
+    e = relerr(download<uint16_t>(ctx, out), want);
+    u16v got_k2 = download<uint16_t>(ctx, kc2);
+    same = true;
+    for (int h = 0; h < Hkv; ++h)
+      same &= !std::memcmp(&got_k2[(size_t(h) * max_seq + start) * D], &ck[(size_t(h) * max_seq + start) * D],
+                           size_t(S) * D * 2);
+    expect(e <= 1e-2 && same, "attention_prefill_write_cache", e);
+    // cached: S2 new queries at positions start+S .. attend the cache rows
+    // [0, start+S+S2): fill rows [0,start) and [start+S, start+S+S2) too
+    u16v full_k = rand_bf16(size_t(Hkv) * max_seq * D), full_v = rand_bf16(size_t(Hkv) * max_seq * D);
+    Tensor fk = upload(ctx, full_k, {Hkv, max_seq, D}, DType::bf16), fv = upload(ctx, full_v, {Hkv, max_seq, D}, DType::bf16);
+    u16v q2 = rand_bf16(size_t(S2) * Hq * D);
+    Tensor tq2 = upload(ctx, q2, {S2, Hq * D}, DType::bf16), out2 = Tensor::allocate(ctx, {S2, Hq * D});
+    ops::attention_prefill_cached(ctx, tq2, fk, fv, out2, scores, S2, start + S, Hq, Hkv, D, max_seq);
+    u16v want2(size_t(S2) * Hq * D);
+    orc_attention_prefill_cached(q2.data(), full_k.data(), full_v.data(), want2.data(), S2, start + S, Hq, Hkv, D,
+                                 max_seq, 0);
+    e = relerr(download<uint16_t>(ctx, out2), want2);
+    expect(e <= 1e-2, "attention_prefill_cached", e);
+    // unsupported head_dim must throw
+    bool threw = false;
+    try {
+      ops::attention_prefill(ctx, tq, tk, tv, out, scores, S, Hq, Hkv, 96);
+    } catch (const std::runtime_error&) {
+      threw = true;
+    }
+    expect(threw, "attention_prefill rejects head_dim 96", 0);
+  }
+  // ---- DeltaNet: prefill then decode steps --------------------------------
+  {
+    const int T = 150, Hk = 2, Hv = 4, d = 128, steps = 3, total = T + steps;
+    const float eps = 1e-6f, scale = 1.0f / std::sqrt(float(d));
+    u16v q = rand_bf16(size_t(total) * Hk * d), k = rand_bf16(size_t(total) * Hk * d),
+         v = rand_bf16(size_t(total) * Hv * d), a = rand_bf16(size_t(total) * Hv), b = rand_bf16(size_t(total) * Hv);
+    std::vector<float> S0(size_t(Hv) * d * d);
+    for (auto& x : S0) x = 0.02f * nrand();
+    Tensor tq = upload(ctx, q, {total, Hk * d}, DType::bf16), tk = upload(ctx, k, {total, Hk * d}, DType::bf16),
+           tv = upload(ctx, v, {total, Hv * d}, DType::bf16), ta = upload(ctx, a, {total, Hv}, DType::bf16),
+           tb = upload(ctx, b, {total, Hv}, DType::bf16);
+    Tensor st = upload(ctx, S0, {1, Hv, d, d}, DType::f32);
+    Tensor out = Tensor::allocate(ctx, {total, Hv * d});
+    Tensor ws = Tensor::allocate(ctx, {int64_t(ops::linear_delta_prefill_workspace_bytes(T, Hv, d, d))}, DType::u8);
+    ops::linear_delta_prefill(ctx, tq, tk, tv, ta, tb, nullptr, nullptr, st, out, ws, T, Hk, Hv, d, d, eps, scale);
+    for (int s = T; s < total; ++s) {
+      Tensor vq = Tensor::view(ctx, tq.data_as<uint16_t>() + size_t(s) * Hk * d, {Hk * d});
+      Tensor vk = Tensor::view(ctx, tk.data_as<uint16_t>() + size_t(s) * Hk * d, {Hk * d});
+      Tensor vv = Tensor::view(ctx, tv.data_as<uint16_t>() + size_t(s) * Hv * d, {Hv * d});
+      Tensor va = Tensor::view(ctx, ta.data_as<uint16_t>() + size_t(s) * Hv, {Hv});
+      Tensor vb = Tensor::view(ctx, tb.data_as<uint16_t>() + size_t(s) * Hv, {Hv});
+      Tensor vo = Tensor::view(ctx, out.data_as<uint16_t>() + size_t(s) * Hv * d, {Hv * d});
+      ops::linear_delta_decode(ctx, vq, vk, vv, va, vb, nullptr, nullptr, st, vo, Hk, Hv, d, d, eps, scale);
+    }
+    std::vector<float> Sw = S0, of(size_t(total) * Hv * d);
+    u16v ob(size_t(total) * Hv * d);
+    orc_deltanet_recurrent(q.data(), k.data(), v.data(), a.data(), b.data(), nullptr, nullptr, Sw.data(), of.data(),
+                           ob.data(), 1, total, Hk, Hv, d, d, eps, scale, 1);
+    double es = relerr_f(download<float>(ctx, st), Sw);
+    double eo = relerr(download<uint16_t>(ctx, out), ob);
+    expect(es <= 1e-3, "linear_delta prefill+decode state", es);
+    expect(eo <= 1e-2, "linear_delta prefill+decode outputs", eo);
+  }
+  std::printf("peak device bytes %zu\n", ctx.peak_allocated_bytes());
+  std::printf(g_fail ? "FAILED %d\n" : "ALL OK\n", g_fail);
+  return g_fail ? 1 : 0;
+}

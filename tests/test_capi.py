@@ -43,6 +43,9 @@ def test_argument_validation_runs_before_any_device_work():
     p = ctypes.c_void_p(16)   # never dereferenced: validation fails first
     rc = l.aila_hip_gqa_decode(p, p, p, p, None, 0, 1, 12, 8, 128, 512, 10, None, None)
     assert rc == -1
+    ws = ctypes.c_void_p(4096)
+    rc = l.aila_hip_gqa_decode(p, p, p, p, ws, 100, 1, 16, 8, 128, 512, 10, None, None)
+    assert rc == -4   # workspace too small for two split records
     rc = l.aila_hip_deltanet_decode(p, p, p, p, p, None, None, p, p, 1, 3, 4, 128, 128,
                                     1e-6, 0.1, None)
     assert rc == -1 and b"Hv % Hk" in l.aila_hip_last_error()
