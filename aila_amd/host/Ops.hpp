@@ -35,7 +35,7 @@ void attention_prefill(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& ou
                        int head_dim);
 
 // attention_prefill fused with the two copy_to_cache calls that precede it in
-// the backends (Qwen3DenseBackend.cpp:320-327): k/v are also written to the
+// the backends (Qwen3DenseBackend.cpp:318-325): k/v are also written to the
 // caches at start_pos. Addition; the reference issues three ops.
 void attention_prefill_write_cache(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& output,
                                    Tensor& k_cache, Tensor& v_cache, int seq_len, int start_pos,

@@ -76,7 +76,7 @@ int aila_hip_kv_append(const void* k_new, const void* v_new, void* k_cache,
  * Replaces ops::attention_prefill (src/ops/Ops.hpp:278-282;
  * src/ops/AttentionOps.cpp:649-842) fused with the two ops::copy_to_cache
  * calls that precede it in the backends (Ops.hpp:199-201,
- * AttentionOps.cpp:2513-2532; Qwen3DenseBackend.cpp:320-327).
+ * AttentionOps.cpp:2513-2532; Qwen3DenseBackend.cpp:318-325).
  *   q [S, Hq*D], k/v [S, Hkv*D] bf16 (token-major, already QK-normed/RoPE'd)
  *   out [S, Hq*D] bf16; query i attends keys [0, i].
  *   k_cache/v_cache [Hkv, max_seq, D] bf16 or both NULL: when given, k/v are
