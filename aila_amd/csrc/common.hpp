@@ -36,9 +36,14 @@ __device__ __forceinline__ bf16 f2bf(float f) {
   return static_cast<bf16>(u >> 16);
 }
 
-// Two fp32 -> packed bf16x2 (low half = a).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16x2 (low half = a), round-to-nearest-even in one
+// v_cvt_pk_bf16_f32 (same results as f2bf for every non-NaN input).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+  const f32x2 f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
 // Unpack 8 bf16 held in a 16-byte vector into fp32.

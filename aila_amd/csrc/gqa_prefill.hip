@@ -31,254 +31,387 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-
-__device__ __forceinline__ int vslot(int k) {
-  // key k (0..BN-1) -> column in the V^T tile
-  return (k & ~31) | (((k & 15) >> 2) << 3) | (((k >> 4) & 1) << 2) | (k & 3);
-}
+constexpr float kLazyRescaleLog2 = 8.0f;
+constexpr int kNumXcd = 8;   // MI355X: 8 accelerator complex dies, one L2 each
+// s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt and lgkmcnt not waited on.
+constexpr int kWaitVmcntZero = 0x0F70;
 
 template <int D, int RPW, int BN>
 struct PrefillCfg {
-  static constexpr int BM = kWaves * RPW;
+  static constexpr int BM = kWaves * RPW;   // query rows of one 4-wave group
   static constexpr int QT = RPW / 16;     // 16-row query tiles per wave
   static constexpr int KS = D / 32;       // MFMA k-steps over D (S^T)
   static constexpr int DT = D / 16;       // 16-row d tiles (O^T)
   static constexpr int KT = BN / 16;      // 16-key tiles per block
   static constexpr int PS = BN / 32;      // 32-key MFMA steps (O^T)
-  static constexpr int KP = D + 8;        // K tile pitch (bf16 elements)
-  static constexpr int VP = BN + 8;       // V^T tile pitch
-  static constexpr int KCH = BN * D / 8 / kThreads;        // 16B K chunks / thread
-  static constexpr int VU = (BN / 4) * (D / 8);            // 4-key x 8-d V units
-  static constexpr int VUT = (VU + kThreads - 1) / kThreads;
+  static constexpr int NC = D / 8;        // 16-byte chunks per K/V row
+  static constexpr int RB = D * 2;        // bytes per K/V row
+  static constexpr int TILE = BN * RB;    // one K or V tile (unpadded, swizzled)
+  static constexpr int GROUP_BYTES = 4 * TILE;              // K, V x 2 buffers
+  static constexpr int LOADS = BN * NC / kThreads;          // 16-byte DMA loads / thread / tile
+  static constexpr int MERGE_HALF = kWaves * QT * (DT / 2) * 64 * 16;   // o_acc half, all waves
   static_assert(BN % 32 == 0 && D % 32 == 0 && RPW % 16 == 0, "tile");
-  static_assert((BN * D / 8) % kThreads == 0, "K chunks");
+  static_assert((BN * NC) % kThreads == 0, "whole DMA waves per tile");
+  static_assert(MERGE_HALF <= 2 * TILE, "merge scratch fits in the buffer-0 K tiles");
+  static_assert(kWaves * QT * 64 * 8 <= 2 * TILE, "m/l scratch fits in the buffer-0 V tiles");
 };
 
+// 16-byte chunk swizzle of K/V tile rows. Tiles are written by direct
+// global->LDS loads (one contiguous KiB per wave instruction, so rows cannot
+// be padded); the XOR keeps both read patterns conflict-free: the S^T A
+// operand (16 rows x one 16-byte chunk) and the transposed V reads (8 rows x
+// one 32-byte chunk pair per half wave).
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);        // 8 chunks per row
+}
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+
+// One workgroup = two 4-wave groups and one head. It owns a balanced pair of
+// query blocks: light block i and heavy block n-1-i (causal work grows with
+// the block index, so every pair costs n+1 key blocks when start_pos = 0).
+// Group A walks the light block's keys and then the first part of the heavy
+// block's keys; group B walks the rest of the heavy block's keys; both run
+// the same number of iterations (within one), each on its own double-buffered
+// K/V tiles, and the heavy block's two partial softmax states are merged
+// through LDS at the end.
+//
+// K and V tiles are row-major [BN][D] in LDS, filled by global_load_lds
+// (no staging registers). O^T += V^T P^T takes its V^T operand from
+// ds_read_b64_tr_b16: within a 16-lane group, lane i addresses 4 bf16 of
+// row kbase + i/4 at column d0 + 4*(i%4), and lane j receives V[kbase+r][d0+j]
+// for r = 0..3 - four keys of one head dim, the A-operand layout.
 template <int D, int RPW, int BN>
-__global__ __launch_bounds__(kThreads, 2) void gqa_prefill_kernel(
+__global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     const bf16* __restrict__ q, int q_row_stride, const bf16* __restrict__ k,
     const bf16* __restrict__ v, int kv_row_stride, long kv_head_stride,
     bf16* __restrict__ out, int o_row_stride, int S, int start_pos, int Hkv,
     int G, float scale_log2, bf16* __restrict__ k_cache,
     bf16* __restrict__ v_cache, int cache_pos, int max_seq) {
   using C = PrefillCfg<D, RPW, BN>;
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * C::KP];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][D * C::VP];
+  // K/V tiles per double-buffer slot, indexed by group.
+  __shared__ __attribute__((aligned(1024))) unsigned char sK0[2][C::TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sK1[2][C::TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sV0[2][C::TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sV1[2][C::TILE];
+
+  const int grp = threadIdx.x / kThreads;               // 0 = A, 1 = B
+  const int t = threadIdx.x % kThreads, lane = t & 63, wave = t >> 6;
+  const int m16 = lane & 15, g4 = lane >> 4;
+  auto tileK = [&](int buf) __attribute__((always_inline)) -> unsigned char* { return buf ? sK1[grp] : sK0[grp]; };
+  auto tileV = [&](int buf) __attribute__((always_inline)) -> unsigned char* { return buf ? sV1[grp] : sV0[grp]; };
 
   const int nqb = (S + C::BM - 1) / C::BM;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);   // heavy blocks first
-  const int h = blockIdx.y;
+  const int npair = (nqb + 1) / 2;
+  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs,
+  // so consecutive logical ids (pairs of one head, then the heads of one KV
+  // group) are gathered onto one XCD and its L2 holds that group's K/V.
+  const int nwg = npair * static_cast<int>(gridDim.y);
+  const int lin = blockIdx.x + npair * blockIdx.y;
+  int logical = lin;
+  if (nwg % kNumXcd == 0) logical = (lin % kNumXcd) * (nwg / kNumXcd) + lin / kNumXcd;
+  const int pr = logical % npair;
+  const int h = logical / npair;
   const int kvh = h / G;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int m16 = lane & 15, g4 = lane >> 4;
-  const int q0 = qb * C::BM;
-  const int q_hi = min(q0 + C::BM, S) - 1;
+  const int ql = pr, qh = nqb - 1 - pr;                  // light / heavy query block
+  auto nkeyblk = [&](int qb) __attribute__((always_inline)) { return (start_pos + min((qb + 1) * C::BM, S) - 1) / BN + 1; };
+  const int nl = (ql < qh) ? nkeyblk(ql) : 0;           // a middle block pairs with itself
+  const int nh = nkeyblk(qh);
+  const int tA = (nl + nh + 1) / 2, tB = nl + nh - tA;
+  const int hsplit = tA - nl;                           // heavy key blocks walked by A
+  const int my_n = grp == 0 ? tA : tB;
+  auto kb_of = [&](int it) __attribute__((always_inline)) { return grp == 0 ? (it < nl ? it : it - nl) : hsplit + it; };
+  auto qb_of = [&](int it) __attribute__((always_inline)) { return (grp == 0 && it < nl) ? ql : qh; };
   const int kv_len = start_pos + S;
-  const int nkb = (start_pos + q_hi) / BN + 1;
   const bf16* Kh = k + kvh * kv_head_stride;
   const bf16* Vh = v + kvh * kv_head_stride;
-  const bool write_cache = (k_cache != nullptr) && (h % G == 0);
+  const bool cache_head = (k_cache != nullptr) && (h % G == 0);
 
-  // ---- Q^T operands (B of S^T), loaded once ------------------------------
+  // ---- K/V block -> LDS by DMA (wave-contiguous KiB per instruction) ------
+  auto issue = [&](int buf, int kb) __attribute__((always_inline)) {
+    const int key0 = kb * BN;
+    unsigned char* tk = tileK(buf);
+    unsigned char* tv = tileV(buf);
+#pragma unroll
+    for (int i = 0; i < C::LOADS; ++i) {
+      const int wchunk = (i * kWaves + wave) * 64;     // first 16-byte slot of this wave instruction
+      const int p = wchunk + lane;
+      const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
+      const size_t goff = static_cast<size_t>(min(key0 + r, kv_len - 1)) * kv_row_stride + qc * 8;
+      __builtin_amdgcn_global_load_lds(Kh + goff, (lds_void_t*)(tk + wchunk * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Vh + goff, (lds_void_t*)(tv + wchunk * 16), 16, 0, 0);
+    }
+  };
+  // The chunk's own key rows of query block qb go to the cache (fused
+  // copy_to_cache), copied out of the LDS tiles.
+  auto write_cache = [&](int buf, int kb, int qb) __attribute__((always_inline)) {
+    const int key0 = kb * BN;
+    const int cq0 = qb * C::BM, cq1 = min(cq0 + C::BM, S) - 1;
+    if (!(cache_head && key0 + BN - 1 >= cq0 && key0 <= cq1)) return;
+    const unsigned char* tk = tileK(buf);
+    const unsigned char* tv = tileV(buf);
+#pragma unroll
+    for (int i = 0; i < C::LOADS; ++i) {
+      const int p = i * kThreads + t;
+      const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
+      const int key = key0 + r;
+      if (key >= cq0 && key <= cq1) {
+        const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + key) * D + qc * 8;
+        *reinterpret_cast<u32x4*>(k_cache + dst) = *reinterpret_cast<const u32x4*>(tk + p * 16);
+        *reinterpret_cast<u32x4*>(v_cache + dst) = *reinterpret_cast<const u32x4*>(tv + p * 16);
+      }
+    }
+  };
+
+  // ---- per-segment state ---------------------------------------------------
   bf16x8_t qb_op[C::QT][C::KS];
-#pragma unroll
-  for (int qt = 0; qt < C::QT; ++qt) {
-    const int row = min(q0 + wave * RPW + qt * 16 + m16, S - 1);
-    const bf16* qr = q + static_cast<size_t>(row) * q_row_stride + h * D + g4 * 8;
-#pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) qb_op[qt][ks] = as_bf16x8(ld16(qr + ks * 32));
-  }
-
-  // ---- global -> register staging of one K/V block -----------------------
-  u32x4 kreg[C::KCH];
-  u32x4 vreg[C::VUT][4];
-  auto fetch = [&](int kb) {
-    const int key0 = kb * BN;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = t + i * kThreads;
-      const int r = c / (D / 8), c8 = c % (D / 8);
-      const int key = min(key0 + r, kv_len - 1);
-      kreg[i] = ld16(Kh + static_cast<size_t>(key) * kv_row_stride + c8 * 8);
-    }
-#pragma unroll
-    for (int u = 0; u < C::VUT; ++u) {
-      const int unit = t + u * kThreads;
-      if (unit < C::VU) {
-        const int kg = unit / (D / 8), dc = unit % (D / 8);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = min(key0 + kg * 4 + j, kv_len - 1);
-          vreg[u][j] = ld16(Vh + static_cast<size_t>(key) * kv_row_stride + dc * 8);
-        }
-      }
-    }
-  };
-  auto stash = [&](int buf, int kb) {
-    const int key0 = kb * BN;
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int c = t + i * kThreads;
-      const int r = c / (D / 8), c8 = c % (D / 8);
-      *reinterpret_cast<u32x4*>(&sK[buf][r * C::KP + c8 * 8]) = kreg[i];
-      if (write_cache) {
-        const int key = key0 + r;
-        if (key >= q0 && key <= q_hi)
-          *reinterpret_cast<u32x4*>(k_cache + (static_cast<size_t>(kvh) * max_seq + cache_pos + key) * D + c8 * 8) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < C::VUT; ++u) {
-      const int unit = t + u * kThreads;
-      if (unit < C::VU) {
-        const int kg = unit / (D / 8), dc = unit % (D / 8);
-        // transpose 4 keys x 8 d into 8 rows of V^T (4 contiguous slots)
-        const int col = vslot(kg * 4);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int w = e >> 1;
-          const bool hi = e & 1;
-          uint32_t x0 = hi ? (vreg[u][0][w] >> 16) : (vreg[u][0][w] & 0xffffu);
-          uint32_t x1 = hi ? (vreg[u][1][w] >> 16) : (vreg[u][1][w] & 0xffffu);
-          uint32_t x2 = hi ? (vreg[u][2][w] >> 16) : (vreg[u][2][w] & 0xffffu);
-          uint32_t x3 = hi ? (vreg[u][3][w] >> 16) : (vreg[u][3][w] & 0xffffu);
-          u32x2 pk = {x0 | (x1 << 16), x2 | (x3 << 16)};
-          *reinterpret_cast<u32x2*>(&sV[buf][(dc * 8 + e) * C::VP + col]) = pk;
-        }
-        if (write_cache) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int key = key0 + kg * 4 + j;
-            if (key >= q0 && key <= q_hi)
-              *reinterpret_cast<u32x4*>(v_cache + (static_cast<size_t>(kvh) * max_seq + cache_pos + key) * D + dc * 8) = vreg[u][j];
-          }
-        }
-      }
-    }
-  };
-
   f32x4 o_acc[C::DT][C::QT];
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-    for (int qt = 0; qt < C::QT; ++qt) o_acc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run[C::QT], l_run[C::QT];
+  int seg_qb = -1;
+  auto begin_segment = [&](int qb) __attribute__((always_inline)) {
+    seg_qb = qb;
 #pragma unroll
-  for (int qt = 0; qt < C::QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-  }
-  int qpos[C::QT];
+    for (int qt = 0; qt < C::QT; ++qt) {
+      const int row = min(qb * C::BM + wave * RPW + qt * 16 + m16, S - 1);
+      const bf16* qr = q + static_cast<size_t>(row) * q_row_stride + h * D + g4 * 8;
 #pragma unroll
-  for (int qt = 0; qt < C::QT; ++qt) qpos[qt] = start_pos + q0 + wave * RPW + qt * 16 + m16;
-  const int wave_qmin = start_pos + q0 + wave * RPW;
+      for (int ks = 0; ks < C::KS; ++ks) qb_op[qt][ks] = as_bf16x8(ld16(qr + ks * 32));
+      m_run[qt] = -INFINITY;
+      l_run[qt] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) o_acc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store_segment = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int qt = 0; qt < C::QT; ++qt) {
+      float l = l_run[qt];
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+      const float inv = 1.0f / l;
+      const int row = seg_qb * C::BM + wave * RPW + qt * 16 + m16;
+      if (row < S) {
+        bf16* orow = out + static_cast<size_t>(row) * o_row_stride + h * D + g4 * 4;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          const f32x4 o = o_acc[dt][qt] * inv;
+          const u32x2 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          *reinterpret_cast<u32x2*>(orow + dt * 16) = w;
+        }
+      }
+    }
+  };
 
-  fetch(0);
-  stash(0, 0);
-  __syncthreads();
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    if (kb + 1 < nkb) fetch(kb + 1);
+  // ---- one key block against the current segment ---------------------------
+  auto compute_block = [&](int buf, int kb) __attribute__((always_inline)) {
     const int key0 = kb * BN;
-    // A wave whose rows all precede this block's first key skips it.
-    if (key0 <= wave_qmin + RPW - 1) {
-      // ---- S^T = K Q^T -----------------------------------------------------
-      f32x4 st[C::KT][C::QT];
+    const int wave_qmin = start_pos + seg_qb * C::BM + wave * RPW;
+    if (key0 > wave_qmin + RPW - 1) return;   // every key of the block is in this wave's future
+    const unsigned char* tk = tileK(buf);
+    const unsigned char* tv = tileV(buf);
+    // S^T = K Q^T; the K operands of k-step ks+1 are read while the MFMAs of
+    // step ks run.
+    auto load_k = [&](int ks, bf16x8_t* ka) __attribute__((always_inline)) {
+#pragma unroll
+      for (int kt = 0; kt < C::KT; ++kt) {
+        const int r = kt * 16 + m16;
+        ka[kt] = as_bf16x8(*reinterpret_cast<const u32x4*>(tk + r * C::RB + (((ks * 4 + g4) ^ swz<D>(r)) << 4)));
+      }
+    };
+    f32x4 st[C::KT][C::QT];
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt)
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8_t ka0[C::KT], ka1[C::KT];
+    load_k(0, ka0);
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      bf16x8_t* cur = (ks & 1) ? ka1 : ka0;
+      bf16x8_t* nxt = (ks & 1) ? ka0 : ka1;
+      if (ks + 1 < C::KS) load_k(ks + 1, nxt);
 #pragma unroll
       for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
-        for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = mfma16x16x32(cur[kt], qb_op[qt][ks], st[kt][qt]);
+    }
+    // V^T operands come from transposing LDS reads.
+    const int vr = 4 * g4 + (m16 >> 2);          // row within a 32-key step (first half)
+    const int vc = 4 * (m16 & 3);                // column offset within a 16-wide d tile
+    auto load_v = [&](int s2, bf16x8_t* va) __attribute__((always_inline)) {
 #pragma unroll
-      for (int ks = 0; ks < C::KS; ++ks) {
+      for (int dt = 0; dt < C::DT; ++dt) {
+        const int d = dt * 16 + vc;
+        const int r0 = s2 * 32 + vr, r1 = r0 + 16;
+        const unsigned char* p0 = tv + r0 * C::RB + (((d >> 3) ^ swz<D>(r0)) << 4) + ((d & 7) << 1);
+        const unsigned char* p1 = tv + r1 * C::RB + (((d >> 3) ^ swz<D>(r1)) << 4) + ((d & 7) << 1);
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p0);
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p1);
+        const u32x4 w = {__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
+                         __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]};
+        va[dt] = as_bf16x8(w);
+      }
+    };
+    // mask (raw scores) and row maxima
+    const bool need_mask = (key0 + BN - 1 > wave_qmin);
+    float alpha[C::QT];
+    bool any_rescale = false;
 #pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-          const bf16x8_t a = as_bf16x8(
-              *reinterpret_cast<const u32x4*>(&sK[buf][(kt * 16 + m16) * C::KP + ks * 32 + g4 * 8]));
+    for (int qt = 0; qt < C::QT; ++qt) {
+      const int qpos = wave_qmin + qt * 16 + m16;
+      float mx = -INFINITY;
 #pragma unroll
-          for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = mfma16x16x32(a, qb_op[qt][ks], st[kt][qt]);
+      for (int kt = 0; kt < C::KT; ++kt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (need_mask && (key0 + kt * 16 + g4 * 4 + j > qpos)) st[kt][qt][j] = -INFINITY;
+          mx = fmaxf(mx, st[kt][qt][j]);
         }
       }
-      // ---- mask, online softmax ------------------------------------------
-      const bool need_mask = (key0 + BN - 1 > wave_qmin);
-      float alpha[C::QT];
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx *= scale_log2;
+      // Lazy rescaling: the reference max only moves when the block max
+      // exceeds it by more than 2^8 (p <= 256 stays exact in fp32 and bf16
+      // range); the normalisation by l is unaffected.
+      const bool grow = mx > m_run[qt] + kLazyRescaleLog2;
+      const float mn = grow ? mx : m_run[qt];
+      alpha[qt] = grow ? ((m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn)) : 1.0f;
+      m_run[qt] = mn;
+      any_rescale |= grow;
+    }
+    // P^T operands: step s2 covers keys 32*s2 + {4g..4g+3, 16+4g..16+4g+3}
+    bf16x8_t pb[C::PS][C::QT];
+    float l_psum[C::QT];
 #pragma unroll
-      for (int qt = 0; qt < C::QT; ++qt) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float s = st[kt][qt][j] * scale_log2;
-            if (need_mask && (key0 + kt * 16 + g4 * 4 + j > qpos[qt])) s = -INFINITY;
-            st[kt][qt][j] = s;
-            mx = fmaxf(mx, s);
-          }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mn = fmaxf(m_run[qt], mx);
-        alpha[qt] = (m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn);
-        m_run[qt] = mn;
-        l_run[qt] *= alpha[qt];
-      }
-      // P^T operands: step s2 covers keys 32*s2 + {4g..4g+3, 16+4g..16+4g+3}
-      bf16x8_t pb[C::PS][C::QT];
+    for (int qt = 0; qt < C::QT; ++qt) {
+      l_psum[qt] = 0.f;
+      const float nm = -m_run[qt];
 #pragma unroll
       for (int s2 = 0; s2 < C::PS; ++s2) {
+        float p[8];
 #pragma unroll
-        for (int qt = 0; qt < C::QT; ++qt) {
-          const float mref = m_run[qt];
-          float p[8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            p[j] = fast_exp2(st[2 * s2][qt][j] - mref);
-            p[4 + j] = fast_exp2(st[2 * s2 + 1][qt][j] - mref);
-          }
-#pragma unroll
-          for (int j = 0; j < 8; ++j) l_run[qt] += p[j];
-          u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                     pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
-          pb[s2][qt] = as_bf16x8(w);
+        for (int j = 0; j < 4; ++j) {
+          p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
+          p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) l_psum[qt] += p[j];
+        const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                         pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
+        pb[s2][qt] = as_bf16x8(w);
       }
-      // ---- O^T = alpha O^T + V^T P^T ---------------------------------------
+    }
+    if (__any(any_rescale)) {
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) {
+        l_run[qt] *= alpha[qt];
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) o_acc[dt][qt] *= alpha[qt];
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < C::QT; ++qt) l_run[qt] += l_psum[qt];
+    // O^T += V^T P^T, one 32-key step at a time.
+#pragma unroll
+    for (int s2 = 0; s2 < C::PS; ++s2) {
+      bf16x8_t va[C::DT];
+      load_v(s2, va);
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-        for (int qt = 0; qt < C::QT; ++qt) o_acc[dt][qt] *= alpha[qt];
-#pragma unroll
-      for (int s2 = 0; s2 < C::PS; ++s2) {
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
-          const bf16x8_t a = as_bf16x8(
-              *reinterpret_cast<const u32x4*>(&sV[buf][(dt * 16 + m16) * C::VP + s2 * 32 + g4 * 8]));
-#pragma unroll
-          for (int qt = 0; qt < C::QT; ++qt) o_acc[dt][qt] = mfma16x16x32(a, pb[s2][qt], o_acc[dt][qt]);
-        }
-      }
+        for (int qt = 0; qt < C::QT; ++qt) o_acc[dt][qt] = mfma16x16x32(va[dt], pb[s2][qt], o_acc[dt][qt]);
     }
-    if (kb + 1 < nkb) stash(buf ^ 1, kb + 1);
+  };
+
+  // ---- main loop: both groups in lock step -----------------------------------
+  if (my_n > 0) {
+    begin_segment(qb_of(0));
+    issue(0, kb_of(0));
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+  __syncthreads();
+  auto iteration = [&](int cur, int nxt, int it) __attribute__((always_inline)) {
+    if (it + 1 < my_n) issue(nxt, kb_of(it + 1));
+    if (it < my_n) {
+      if (cache_head) write_cache(cur, kb_of(it), qb_of(it));
+      compute_block(cur, kb_of(it));
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);   // the DMA into the other buffer has landed
     __syncthreads();
+  };
+  auto run = [&](int it0, int it1) __attribute__((always_inline)) {
+    for (int it = it0; it < it1; ++it) iteration(it & 1, (it + 1) & 1, it);
+  };
+  // Two loops split at the light/heavy switch of group A, so no loop body
+  // holds a Q reload.
+  const int it_switch = (nl > 0 && hsplit > 0) ? nl : tA;
+  run(0, it_switch);
+  if (it_switch < tA) {
+    if (grp == 0) {
+      store_segment();
+      begin_segment(qh);
+    }
+    run(it_switch, tA);
   }
 
-  // ---- epilogue: normalise, bf16, store ----------------------------------
+  // ---- finish: light block of A, heavy block (merged when split) -------------
+  const bool a_has_heavy = hsplit > 0;
+  const bool b_has_heavy = tB > 0;
+  if (grp == 0 && !a_has_heavy && nl > 0) store_segment();          // A only had the light block
+  if (a_has_heavy && b_has_heavy) {
+    // A publishes its heavy partial state; B merges and stores. The o_acc
+    // exchange goes in two halves of the d tiles through the buffer-0 K
+    // tiles; m and l through the buffer-0 V tiles.
+    float* o_scr = reinterpret_cast<float*>(&sK0[0][0]) + wave * (C::QT * (C::DT / 2) * 64 * 4);
+    float* ml_scr = reinterpret_cast<float*>(&sV0[0][0]) + wave * (C::QT * 64 * 2);
+    float fa[C::QT], fb[C::QT];
+    if (grp == 0) {
 #pragma unroll
-  for (int qt = 0; qt < C::QT; ++qt) {
-    float l = l_run[qt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
-    const int row = q0 + wave * RPW + qt * 16 + m16;
-    if (row < S) {
-      bf16* orow = out + static_cast<size_t>(row) * o_row_stride + h * D + g4 * 4;
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
-        const f32x4 o = o_acc[dt][qt] * inv;
-        u32x2 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-        *reinterpret_cast<u32x2*>(orow + dt * 16) = w;
+      for (int qt = 0; qt < C::QT; ++qt) {
+        ml_scr[(qt * 64 + lane) * 2] = m_run[qt];
+        ml_scr[(qt * 64 + lane) * 2 + 1] = l_run[qt];
       }
     }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      if (grp == 0) {
+#pragma unroll
+        for (int qt = 0; qt < C::QT; ++qt)
+#pragma unroll
+          for (int dd = 0; dd < C::DT / 2; ++dd)
+            *reinterpret_cast<f32x4*>(&o_scr[((qt * (C::DT / 2) + dd) * 64 + lane) * 4]) = o_acc[half * (C::DT / 2) + dd][qt];
+      }
+      __syncthreads();
+      if (grp == 1) {
+#pragma unroll
+        for (int qt = 0; qt < C::QT; ++qt) {
+          if (half == 0) {
+            const float ma = ml_scr[(qt * 64 + lane) * 2], la = ml_scr[(qt * 64 + lane) * 2 + 1];
+            const float M = fmaxf(ma, m_run[qt]);
+            fa[qt] = (ma == -INFINITY) ? 0.f : fast_exp2(ma - M);
+            fb[qt] = (m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - M);
+            l_run[qt] = fa[qt] * la + fb[qt] * l_run[qt];
+          }
+#pragma unroll
+          for (int dd = 0; dd < C::DT / 2; ++dd) {
+            const int dt = half * (C::DT / 2) + dd;
+            o_acc[dt][qt] = fa[qt] * *reinterpret_cast<const f32x4*>(&o_scr[((qt * (C::DT / 2) + dd) * 64 + lane) * 4]) +
+                            fb[qt] * o_acc[dt][qt];
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (grp == 1) store_segment();
+  } else if (a_has_heavy && grp == 0) {
+    store_segment();
+  } else if (b_has_heavy && grp == 1) {
+    store_segment();
   }
 }
 
@@ -289,8 +422,9 @@ int launch_prefill(const bf16* q, const bf16* k, const bf16* v, int kv_row_strid
                    hipStream_t st) {
   using C = PrefillCfg<D, RPW, BN>;
   const int nqb = (S + C::BM - 1) / C::BM;
+  const int npair = (nqb + 1) / 2;
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-  hipLaunchKernelGGL((gqa_prefill_kernel<D, RPW, BN>), dim3(nqb, Hq), dim3(kThreads), 0, st,
+  hipLaunchKernelGGL((gqa_prefill_kernel<D, RPW, BN>), dim3(npair, Hq), dim3(2 * kThreads), 0, st,
                      q, Hq * D, k, v, kv_row_stride, kv_head_stride, out, Hq * D, S, start_pos,
                      Hkv, Hq / Hkv, scale_log2, k_cache, v_cache, cache_pos, max_seq);
   return check_launch("gqa_prefill");

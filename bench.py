@@ -394,9 +394,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-sub", action="store_true", help="skip the config 1-4 sub-metrics")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--profile-kernel", action="store_true",
-                    help="only run the dominant kernel (config-5 GQA decode layer, L=32768) and a "
-                         "1 GiB device copy, 20 times each, for rocprofv3 counter runs")
+    ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
+                    choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill"],
+                    help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
+                         "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path "
@@ -409,7 +410,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
 
     if args.profile_kernel:
-        profile_kernel(torch, aila_amd)
+        {"gqa_decode": profile_kernel, "gqa_prefill": lambda t, a: sub_prefill(t, a, reps=20),
+         "deltanet_decode": lambda t, a: sub_deltanet_decode(t, a, steps=320),
+         "deltanet_prefill": lambda t, a: sub_deltanet_prefill(t, a, reps=20)}[args.profile_kernel](torch, aila_amd)
         return
     log(f"[bench] config 5: {args.warmup} warmup + {args.steps} timed steps")
     r5 = bench_config5(torch, aila_amd, args.steps, args.warmup)
