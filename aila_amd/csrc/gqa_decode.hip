@@ -30,9 +30,22 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kTokPerWaveIter = 32;   // two MFMA column groups of 16 tokens
+constexpr int kChunk = 16;            // tokens per wave iteration (one MFMA column group)
+constexpr int kNontemporal = 2;       // cache-policy bit for streamed K/V (read once)
+// s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt and lgkmcnt not waited on.
+constexpr int kWaitVmcntZero = 0x0F70;
 constexpr int kMaxSplits = 256;
 constexpr int kRecHeader = 16;
+
+// Chunk swizzle of the per-wave K stage rows (16 rows x D/8 16-byte chunks):
+// the 16 rows read by one MFMA operand load hit 16 distinct bank groups.
+template <int D>
+__device__ __forceinline__ int kswz(int r) {
+  if constexpr (D >= 128) return r & 15;
+  else return (r >> 1) & 7;
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
@@ -47,6 +60,9 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   constexpr int VL = D / 8;           // lanes per V row (16 B each)
   constexpr int VR = 64 / VL;         // V rows per load instruction
   constexpr int GR = (G + 3) / 4;     // 16-lane rows holding score heads
+  constexpr int NC = D / 8;           // 16-byte chunks per row
+  constexpr int STAGE = kChunk * D * 2;          // bytes of one K stage (16 rows)
+  constexpr int NDMA = STAGE / 1024;             // DMA instructions per stage per wave
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   int len = L;
@@ -64,9 +80,12 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   const bf16* V = vc + kv_off;
   const int h0 = kvh * G;             // first query head of the group
 
-  __shared__ float s_p[kWaves][kTokPerWaveIter][G];
-  __shared__ float s_acc[kWaves][G][D];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k[kWaves][2][STAGE];
+  __shared__ float s_p[kWaves][kChunk][G];
   __shared__ float s_ml[kWaves][2][G];
+  static_assert(sizeof(float) * kWaves * G * D <= sizeof(s_k), "epilogue reuses the K ring");
+  // epilogue: per-wave accumulators, in the (then idle) K ring
+  float (*s_acc)[G][D] = reinterpret_cast<float (*)[G][D]>(&s_k[0][0][0]);
 
   // Query operand (A rows = heads, zero rows for m16 >= G).
   bf16x8_t qa[KS];
@@ -88,29 +107,54 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   const int vd = (lane % VL) * 8;
   const int vr = lane / VL;
 
-  for (int t0 = s0 + wave * kTokPerWaveIter; t0 < s1; t0 += kWaves * kTokPerWaveIter) {
-    // ---- scores: two 16-token column groups --------------------------
-    f32x4 sc[2];
+  // K rows of one 16-token chunk -> this wave's LDS stage, whole rows per
+  // DMA instruction (lane order within a row follows the swizzle).
+  auto dma_k = [&](int stage, int t0) __attribute__((always_inline)) {
+    unsigned char* dst = s_k[wave][stage];
 #pragma unroll
-    for (int grp = 0; grp < 2; ++grp) {
-      const int tok = min(t0 + grp * 16 + m16, s1 - 1);   // clamp: always a valid row
-      const bf16* krow = K + static_cast<size_t>(tok) * D + g4 * 8;
-      u32x4 kb[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kb[ks] = ld16(krow + ks * 32);
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32(qa[ks], as_bf16x8(kb[ks]), c);
-      const bool valid = (t0 + grp * 16 + m16) < s1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sc[grp][j] = valid ? c[j] * scale_log2 : -INFINITY;
+    for (int i = 0; i < NDMA; ++i) {
+      const int p = i * 64 + lane;
+      const int r = p / NC, qc = (p % NC) ^ kswz<D>(r);
+      const int tok = min(t0 + r, s1 - 1);
+      __builtin_amdgcn_global_load_lds(K + static_cast<size_t>(tok) * D + qc * 8,
+                                       (lds_void_t*)(dst + i * 1024), 16, 0, kNontemporal);
     }
-    // ---- online softmax (log2 domain) ---------------------------------
+  };
+
+  int t0 = s0 + wave * kChunk;
+  if (t0 < s1) dma_k(0, t0);
+  for (int it = 0; t0 < s1; ++it, t0 += kWaves * kChunk) {
+    const int stage = it & 1;
+    // ---- K operands of this chunk (its DMA was issued one chunk earlier) --
+    const unsigned char* ks_base = s_k[wave][stage];
+    u32x4 kb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kb[ks] = *reinterpret_cast<const u32x4*>(ks_base + m16 * (D * 2) + (((ks * 4 + g4) ^ kswz<D>(m16)) << 4));
+    // ---- V rows of this chunk: nontemporal register loads, issued before
+    //      the next K DMA so waiting on V never waits on that prefetch ------
+    u32x4 vv[kChunk / VR];
+#pragma unroll
+    for (int i = 0; i < kChunk / VR; ++i) {
+      const int tok = min(t0 + vr + i * VR, s1 - 1);
+      vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(V + static_cast<size_t>(tok) * D + vd));
+    }
+    const int t_next = t0 + kWaves * kChunk;
+    if (t_next < s1) dma_k(stage ^ 1, t_next);
+    // ---- scores on MFMA ------------------------------------------------------
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) c = mfma16x16x32(qa[ks], as_bf16x8(kb[ks]), c);
+    const bool valid = (t0 + m16) < s1;
+    float sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = valid ? c[j] * scale_log2 : -INFINITY;
+    // ---- online softmax (log2 domain) ---------------------------------------
     float alpha[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       const int j = h & 3, row = h >> 2;
-      float bm = row16_max(fmaxf(sc[0][j], sc[1][j]));
+      float bm = row16_max(sc[j]);
       bm = readlane_f(bm, row * 16);
       const float mn = fmaxf(m_run[h], bm);
       alpha[h] = (m_run[h] == -INFINITY) ? 0.f : fast_exp2(m_run[h] - mn);
@@ -126,12 +170,9 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
           const int h = r * 4 + j;
           if (h < G) {
             const float mref = (m_run[h] == -INFINITY) ? 0.f : m_run[h];
-#pragma unroll
-            for (int grp = 0; grp < 2; ++grp) {
-              const float p = fast_exp2(sc[grp][j] - mref);
-              l_part[h] += p;
-              s_p[wave][grp * 16 + m16][h] = p;
-            }
+            const float p = fast_exp2(sc[j] - mref);
+            l_part[h] += p;
+            s_p[wave][m16][h] = p;
           }
         }
       }
@@ -139,30 +180,31 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- P.V -----------------------------------------------------------
+    // ---- P.V ------------------------------------------------------------------
 #pragma unroll
     for (int h = 0; h < G; ++h) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
     }
-#pragma unroll 4
-    for (int i = vr; i < kTokPerWaveIter; i += VR) {
-      const int tok = min(t0 + i, s1 - 1);
+#pragma unroll
+    for (int i = 0; i < kChunk / VR; ++i) {
       float vf[8];
-      unpack8(ld16(V + static_cast<size_t>(tok) * D + vd), vf);
+      unpack8(vv[i], vf);
       float p[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) p[h] = s_p[wave][i][h];
+      for (int h = 0; h < G; ++h) p[h] = s_p[wave][vr + i * VR][h];
 #pragma unroll
       for (int h = 0; h < G; ++h) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] += p[h] * vf[e];
       }
     }
-    // The next iteration overwrites this wave's P slice.
+    // The next iteration overwrites this wave's P slice and reads the other
+    // K stage, whose DMA must have landed.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
   }
 
   // ---- wave epilogue --------------------------------------------------
@@ -185,6 +227,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
       acc[h][e] = x;
     }
   }
+  __syncthreads();   // every wave is done with the K ring before it becomes s_acc
   if (vr == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -336,7 +379,7 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache,
     nsplit = 1;
   } else if (workspace) {
     // Aim for ~2048 workgroups (8 per CU on 256 CUs); splits are multiples
-    // of 128 rows (one pass of the four waves).
+    // of 128 rows.
     const int groups = B * Hkv;
     int want = (2048 + groups - 1) / groups;
     want = max(1, min(want, nsplit_max));
