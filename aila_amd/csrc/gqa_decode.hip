@@ -274,10 +274,15 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 
 // Merge of split records, AttentionOps.cpp:276-319: M = max m_i,
 // out = sum_i e^(m_i - M) acc_i / sum_i e^(m_i - M) l_i.
+// Thread t owns 4 head dims (float4 column c) of the splits i = part (mod P),
+// so its record reads are independent and issued together; the P partial
+// sums meet in LDS.
 template <int D>
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
     const float* __restrict__ part, bf16* __restrict__ out, int Hq, int L,
     const int* __restrict__ seq_lens, int split_len, int nsplit_max) {
+  constexpr int C4 = D / 4;             // float4 columns
+  constexpr int P = 256 / C4;           // split phases
   const int hq = blockIdx.x, b = blockIdx.y;
   int len = L;
   if (seq_lens) len = min(max(seq_lens[b], 0), L);
@@ -285,6 +290,7 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
   const float* rec0 = part + (static_cast<size_t>(b) * Hq + hq) * nsplit_max * (kRecHeader + D);
   __shared__ float s_f[kMaxSplits];
   __shared__ float s_inv;
+  __shared__ f32x4 s_red[P][C4];
   // One wave computes the split factors.
   if (threadIdx.x < 64) {
     float M = -INFINITY;
@@ -303,11 +309,32 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
     if (threadIdx.x == 0) s_inv = Ls > 0.f ? 1.0f / Ls : 0.f;
   }
   __syncthreads();
-  const float inv = s_inv;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float A = 0.f;
-    for (int i = 0; i < ns; ++i) A += s_f[i] * rec0[static_cast<size_t>(i) * (kRecHeader + D) + kRecHeader + d];
-    out[(static_cast<size_t>(b) * Hq + hq) * D + d] = f2bf(A * inv);
+  const int c = threadIdx.x % C4, ph = threadIdx.x / C4;
+  f32x4 a = {0.f, 0.f, 0.f, 0.f};
+  constexpr int U = 8;
+  for (int i0 = ph; i0 < ns; i0 += P * U) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * P;
+      v[u] = (i < ns) ? *reinterpret_cast<const f32x4*>(rec0 + static_cast<size_t>(i) * (kRecHeader + D) + kRecHeader + 4 * c)
+                      : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * P;
+      if (i < ns) a += s_f[i] * v[u];
+    }
+  }
+  s_red[ph][c] = a;
+  __syncthreads();
+  if (threadIdx.x < C4) {
+    f32x4 r = s_red[0][threadIdx.x];
+#pragma unroll
+    for (int p2 = 1; p2 < P; ++p2) r += s_red[p2][threadIdx.x];
+    r *= s_inv;
+    const u32x2 w = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+    *reinterpret_cast<u32x2*>(out + (static_cast<size_t>(b) * Hq + hq) * D + 4 * threadIdx.x) = w;
   }
 }
 
