@@ -27,6 +27,7 @@ _SIGS = {
     "aila_hip_version": ([], _I),
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_gqa_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_kv_append": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_prefill": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_gqa_prefill_cached": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -128,6 +129,35 @@ def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
                                    _ptr(workspace), ws_bytes, B, Hq, Hkv, D, max_seq,
                                    int(cached_len), _ptr(seq_lens), _stream(stream))
     _check(rc, "aila_hip_gqa_decode")
+    return out
+
+
+def gqa_decode_append(q, k_new, v_new, k_cache, v_cache, pos: int, out=None, workspace=None,
+                      positions=None, stream=None):
+    """Write k_new/v_new [B,Hkv,D] to cache row pos (or positions[b] <= pos)
+    and attend rows [0, row] -> out [B,Hq,D]."""
+    import torch
+    B, Hq, D = q.shape
+    Hkv, max_seq = k_cache.shape[1], k_cache.shape[2]
+    _need(q, torch.bfloat16, (B, Hq, D), "q")
+    _need(k_new, torch.bfloat16, (B, Hkv, D), "k_new")
+    _need(v_new, torch.bfloat16, (B, Hkv, D), "v_new")
+    _need(k_cache, torch.bfloat16, (B, Hkv, max_seq, D), "k_cache")
+    _need(v_cache, torch.bfloat16, (B, Hkv, max_seq, D), "v_cache")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.bfloat16, (B, Hq, D), "out")
+    ws_bytes = 0
+    if workspace is not None:
+        if not workspace.is_cuda or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous device tensor")
+        ws_bytes = workspace.numel() * workspace.element_size()
+    if positions is not None:
+        _need(positions, torch.int32, (B,), "positions", align=4)
+    rc = lib().aila_hip_gqa_decode_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache),
+                                          _ptr(out), _ptr(workspace), ws_bytes, B, Hq, Hkv, D, max_seq,
+                                          int(pos), _ptr(positions), _stream(stream))
+    _check(rc, "aila_hip_gqa_decode_append")
     return out
 
 

@@ -52,8 +52,8 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kc,
     const bf16* __restrict__ vc, bf16* __restrict__ out,
     float* __restrict__ part, int Hq, int Hkv, int max_seq, int L,
-    const int* __restrict__ seq_lens, int split_len, int nsplit_max,
-    float scale_log2) {
+    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max,
+    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new) {
   static_assert(D % 32 == 0 && D <= 256, "D");
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "G");
   constexpr int KS = D / 32;          // MFMA k-steps over the head dim
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   int len = L;
-  if (seq_lens) len = min(max(seq_lens[b], 0), L);
+  if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
   const int s0 = split * split_len;
   const int nsplit_b = (len + split_len - 1) / split_len;
   const bool single = (part == nullptr);
@@ -120,6 +120,21 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
                                        (lds_void_t*)(dst + i * 1024), 16, 0, kNontemporal);
     }
   };
+
+  // Fused append (decode_prepare's cache write): the workgroup owning the
+  // last row writes the new token's K and V there before anything reads it.
+  if (k_new != nullptr && len > 0 && split == nsplit_b - 1) {
+    if (wave == 0 && lane < 2 * NC) {
+      const int row = len - 1;
+      const bool isv = lane >= NC;
+      const int c = isv ? lane - NC : lane;
+      const bf16* src = (isv ? v_new : k_new) + (static_cast<size_t>(b) * Hkv + kvh) * D + c * 8;
+      bf16* dst = const_cast<bf16*>(isv ? V : K) + static_cast<size_t>(row) * D + c * 8;
+      *reinterpret_cast<u32x4*>(dst) = ld16(src);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+    }
+    __syncthreads();
+  }
 
   int t0 = s0 + wave * kChunk;
   if (t0 < s1) dma_k(0, t0);
@@ -280,12 +295,12 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 template <int D>
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
     const float* __restrict__ part, bf16* __restrict__ out, int Hq, int L,
-    const int* __restrict__ seq_lens, int split_len, int nsplit_max) {
+    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max) {
   constexpr int C4 = D / 4;             // float4 columns
   constexpr int P = 256 / C4;           // split phases
   const int hq = blockIdx.x, b = blockIdx.y;
   int len = L;
-  if (seq_lens) len = min(max(seq_lens[b], 0), L);
+  if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
   const int ns = (len + split_len - 1) / split_len;
   const float* rec0 = part + (static_cast<size_t>(b) * Hq + hq) * nsplit_max * (kRecHeader + D);
   __shared__ float s_f[kMaxSplits];
@@ -338,32 +353,95 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
   }
 }
 
+// Launch arguments shared by the decode entry points.
+struct DecodeArgs {
+  const bf16* q;
+  const bf16* kc;
+  const bf16* vc;
+  bf16* out;
+  float* part;
+  int B, Hq, Hkv, max_seq, L;
+  const int* seq_lens;
+  int len_bias;          // sequence b attends min(seq_lens[b] + len_bias, L) rows
+  int split_len, nsplit, nsplit_max;
+  const bf16* k_new;     // fused append (null: none)
+  const bf16* v_new;
+};
+
 template <int D, int G>
-int launch_decode(const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
-                  float* part, int B, int Hq, int Hkv, int max_seq, int L,
-                  const int* seq_lens, int split_len, int nsplit, int nsplit_max,
-                  hipStream_t st) {
+int launch_decode(const DecodeArgs& a, hipStream_t st) {
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-  hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(nsplit, Hkv, B), dim3(kThreads), 0, st,
-                     q, kc, vc, out, part, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit_max,
-                     scale_log2);
-  if (part) {
-    hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(Hq, B), dim3(256), 0, st, part, out, Hq,
-                       L, seq_lens, split_len, nsplit_max);
+  hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
+                     a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
+                     a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new);
+  if (a.part) {
+    hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
+                       a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit_max);
   }
   return check_launch("gqa_decode");
 }
 
 template <int D>
-int dispatch_g(int G, const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
-               float* part, int B, int Hq, int Hkv, int max_seq, int L,
-               const int* seq_lens, int split_len, int nsplit, int nsplit_max, hipStream_t st) {
+int dispatch_g(int G, const DecodeArgs& a, hipStream_t st) {
   switch (G) {
-    case 1: return launch_decode<D, 1>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
-    case 2: return launch_decode<D, 2>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
-    case 4: return launch_decode<D, 4>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
-    case 8: return launch_decode<D, 8>(q, kc, vc, out, part, B, Hq, Hkv, max_seq, L, seq_lens, split_len, nsplit, nsplit_max, st);
+    case 1: return launch_decode<D, 1>(a, st);
+    case 2: return launch_decode<D, 2>(a, st);
+    case 4: return launch_decode<D, 4>(a, st);
+    case 8: return launch_decode<D, 8>(a, st);
     default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: Hq/Hkv=%d not in {1,2,4,8}", G);
+  }
+}
+
+// Validation, split planning and dispatch for both decode entry points.
+int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, void* workspace,
+                    size_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_seq, int cached_len,
+                    const int* seq_lens, int len_bias, const void* k_new, const void* v_new,
+                    hipStream_t st) {
+  AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
+  AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
+               "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
+  AILA_REQUIRE(cached_len >= 0 && cached_len <= max_seq,
+               "gqa_decode: cached_len=%d outside [0, max_seq=%d]", cached_len, max_seq);
+  DecodeArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.kc = static_cast<const bf16*>(k_cache);
+  a.vc = static_cast<const bf16*>(v_cache);
+  a.out = static_cast<bf16*>(out);
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_seq = max_seq; a.L = cached_len;
+  a.seq_lens = seq_lens; a.len_bias = len_bias;
+  a.k_new = static_cast<const bf16*>(k_new);
+  a.v_new = static_cast<const bf16*>(v_new);
+  // Records per (sequence, head) that the workspace holds; the split count
+  // adapts to it (the reference's [Hq, max_tiles, 272] partials buffer for
+  // D=256 is accepted as-is).
+  const size_t rec_bytes = static_cast<size_t>(B) * Hq * (kRecHeader + D) * sizeof(float);
+  a.nsplit_max = workspace ? static_cast<int>(std::min<size_t>(workspace_bytes / rec_bytes, kMaxSplits)) : 0;
+  if (workspace && a.nsplit_max < 2)
+    return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu bytes holds < 2 split records (%zu bytes each)",
+                     workspace_bytes, rec_bytes);
+  if (cached_len == 0) {
+    // Nothing to attend: the single-pass kernel writes a zero output.
+    a.split_len = 1;
+    a.nsplit = 1;
+  } else if (workspace) {
+    // Aim for ~2048 workgroups (8 per CU on 256 CUs); splits are multiples
+    // of 128 rows.
+    const int groups = B * Hkv;
+    int want = (2048 + groups - 1) / groups;
+    want = std::max(1, std::min(want, a.nsplit_max));
+    a.split_len = (cached_len + want - 1) / want;
+    a.split_len = ((a.split_len + 127) / 128) * 128;
+    a.nsplit = (cached_len + a.split_len - 1) / a.split_len;
+    if (a.nsplit > 1) a.part = static_cast<float*>(workspace);   // one split: direct output
+  } else {
+    a.split_len = cached_len;
+    a.nsplit = 1;
+  }
+  switch (D) {
+    case 64: return dispatch_g<64>(Hq / Hkv, a, st);
+    case 128: return dispatch_g<128>(Hq / Hkv, a, st);
+    case 256: return dispatch_g<256>(Hq / Hkv, a, st);
+    default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: D=%d not in {64,128,256}", D);
   }
 }
 
@@ -375,59 +453,22 @@ extern "C" size_t aila_hip_gqa_decode_workspace_size(int B, int Hq, int D) {
   return static_cast<size_t>(B) * Hq * aila::kMaxSplits * (aila::kRecHeader + D) * sizeof(float);
 }
 
-extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache,
-                                   const void* v_cache, void* out,
-                                   void* workspace, size_t workspace_bytes,
-                                   int B, int Hq, int Hkv, int D, int max_seq,
-                                   int cached_len, const int* seq_lens,
-                                   void* stream) {
+extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                   void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int D,
+                                   int max_seq, int cached_len, const int* seq_lens, void* stream) {
+  return aila::gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq,
+                               cached_len, seq_lens, 0, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aila_hip_gqa_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache,
+                                          void* v_cache, void* out, void* workspace, size_t workspace_bytes,
+                                          int B, int Hq, int Hkv, int D, int max_seq, int pos,
+                                          const int* positions, void* stream) {
   using namespace aila;
-  AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
-  AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
-               "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
-  AILA_REQUIRE(cached_len >= 0 && cached_len <= max_seq,
-               "gqa_decode: cached_len=%d outside [0, max_seq=%d]", cached_len, max_seq);
-  const int G = Hq / Hkv;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  bf16* o = static_cast<bf16*>(out);
-  float* part = nullptr;
-  int split_len, nsplit;
-  // Records per (sequence, head) that the workspace holds; the split count
-  // adapts to it (the reference's [Hq, max_tiles, 272] partials buffer for
-  // D=256 is accepted as-is).
-  const size_t rec_bytes = static_cast<size_t>(B) * Hq * (kRecHeader + D) * sizeof(float);
-  const int nsplit_max = workspace ? static_cast<int>(std::min<size_t>(workspace_bytes / rec_bytes, kMaxSplits)) : 0;
-  if (workspace && nsplit_max < 2)
-    return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu bytes holds < 2 split records (%zu bytes each)",
-                     workspace_bytes, rec_bytes);
-  if (cached_len == 0) {
-    // Nothing to attend: the single-pass kernel writes a zero output.
-    split_len = 1;
-    nsplit = 1;
-  } else if (workspace) {
-    // Aim for ~2048 workgroups (8 per CU on 256 CUs); splits are multiples
-    // of 128 rows.
-    const int groups = B * Hkv;
-    int want = (2048 + groups - 1) / groups;
-    want = max(1, min(want, nsplit_max));
-    split_len = (cached_len + want - 1) / want;
-    split_len = ((split_len + 127) / 128) * 128;
-    nsplit = (cached_len + split_len - 1) / split_len;
-    if (nsplit == 1) part = nullptr;   // one split: write the output directly
-    else part = static_cast<float*>(workspace);
-  } else {
-    split_len = cached_len;
-    nsplit = 1;
-  }
-  const bf16* qp = static_cast<const bf16*>(q);
-  const bf16* kp = static_cast<const bf16*>(k_cache);
-  const bf16* vp = static_cast<const bf16*>(v_cache);
-  switch (D) {
-    case 64: return dispatch_g<64>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, nsplit_max, st);
-    case 128: return dispatch_g<128>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, nsplit_max, st);
-    case 256: return dispatch_g<256>(G, qp, kp, vp, o, part, B, Hq, Hkv, max_seq, cached_len, seq_lens, split_len, nsplit, nsplit_max, st);
-    default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: D=%d not in {64,128,256}", D);
-  }
+  AILA_REQUIRE(k_new && v_new, "gqa_decode_append: null k_new/v_new");
+  AILA_REQUIRE(pos >= 0 && pos < max_seq, "gqa_decode_append: pos=%d outside [0, max_seq=%d)", pos, max_seq);
+  return gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, pos + 1,
+                         positions, 1, k_new, v_new, static_cast<hipStream_t>(stream));
 }
 
 namespace aila {

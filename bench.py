@@ -6,7 +6,8 @@ attention stack, 32 layers in a 3:1 pattern (24 Gated DeltaNet layers with
 16 qk / 32 v heads, dk = dv = 128, fp32 state; 8 GQA layers with 16 q / 4 kv
 heads, head_dim 256, bf16 KV cache), batch 8, context 32768, one new token
 per step. A step is one token through all 32 layers: for each GQA layer the
-new K/V row is appended and split-K decode runs over the cache; for each
+new K/V row is appended and split-K decode runs over the cache (one fused
+launch); for each
 DeltaNet layer the state is updated once. value = algorithmic HBM bytes per
 step / step time (GB/s). Steps are replayed from HIP graphs (device-side
 lengths advance inside the graph), so host launch overhead is not timed.
@@ -119,9 +120,8 @@ def step5(aila_amd, W, p):
     for layer in range(N_LAYERS):
         x = W["pool"][p][layer]
         if layer % 4 == 3:
-            aila_amd.kv_append(x["k"], x["v"], W["kc"][gi], W["vc"][gi], positions=W["positions"])
-            aila_amd.gqa_decode(x["q"], W["kc"][gi], W["vc"][gi], W["max_seq"], out=W["gqa_out"],
-                                workspace=W["ws"], seq_lens=W["lens"])
+            aila_amd.gqa_decode_append(x["q"], x["k"], x["v"], W["kc"][gi], W["vc"][gi], W["max_seq"] - 1,
+                                       out=W["gqa_out"], workspace=W["ws"], positions=W["positions"])
             gi += 1
         else:
             aila_amd.deltanet_decode(x["q"], x["k"], x["v"], x["a"], x["b"], W["states"][di],

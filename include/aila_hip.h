@@ -62,6 +62,22 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int B, int Hq, int Hkv, int D, int max_seq,
                         int cached_len, const int* seq_lens, void* stream);
 
+/* Decode step with the new token's K/V append fused in (the cache write of
+ * ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:105-216, followed by
+ * ops::attention_decode with cached_len = start_pos + 1, as the backends call
+ * them at Qwen35HybridTextBackend.cpp:2109 and :2176).
+ *   k_new/v_new [B, Hkv, D] bf16 are written to cache row `pos` of every
+ *   sequence (or row positions[b] when the optional device int[B]
+ *   `positions` is given; then every positions[b] must be <= pos, which only
+ *   sizes the launch), and sequence b attends rows [0, row].
+ * Other arguments as aila_hip_gqa_decode. */
+int aila_hip_gqa_decode_append(const void* q, const void* k_new,
+                               const void* v_new, void* k_cache,
+                               void* v_cache, void* out, void* workspace,
+                               size_t workspace_bytes, int B, int Hq, int Hkv,
+                               int D, int max_seq, int pos,
+                               const int* positions, void* stream);
+
 /* Append one decoded token's K and V per sequence to the cache (the
  * cache-write half of ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:
  * 105-216, without the norm/RoPE): k_new/v_new [B, Hkv, D] bf16 ->

@@ -189,3 +189,55 @@ def test_kv_append_bit_exact():
     for p in range(max_seq):
         if p not in touched:
             assert not k_np[:, :, p].any()
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_decode_append_fused(split):
+    """gqa_decode_append == kv_append + gqa_decode (bit-exact) and matches the
+    oracle's decode over the appended cache."""
+    import torch
+    import aila_amd
+    B, Hq, Hkv, D, max_seq = 3, 16, 4, 256, 1200
+    pos_list = [1100, 0, 517]
+    q = dg.normal_bf16(4200, 0, (B, Hq, D))
+    kc = dg.normal_bf16(4200, 1, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(4200, 2, (B, Hkv, max_seq, D))
+    kn = dg.normal_bf16(4200, 3, (B, Hkv, D))
+    vn = dg.normal_bf16(4200, 4, (B, Hkv, D))
+    ws = (torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+          if split else None)
+    pos = torch.tensor(pos_list, dtype=torch.int32, device="cuda")
+    k1, v1 = _t(kc), _t(vc)
+    out1 = aila_amd.gqa_decode_append(_t(q), _t(kn), _t(vn), k1, v1, max(pos_list), workspace=ws, positions=pos)
+    k2, v2 = _t(kc), _t(vc)
+    aila_amd.kv_append(_t(kn), _t(vn), k2, v2, positions=pos)
+    lens = torch.tensor([p + 1 for p in pos_list], dtype=torch.int32, device="cuda")
+    out2 = aila_amd.gqa_decode(_t(q), k2, v2, max(pos_list) + 1, workspace=ws, seq_lens=lens)
+    torch.cuda.synchronize()
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(out1, out2)
+    got = dg.bf16_to_f32(_np_bf16(out1))
+    for b, p in enumerate(pos_list):
+        kc[b, :, p] = kn[b]
+        vc[b, :, p] = vn[b]
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(q[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq,
+                                                               Hkv, D, max_seq, p + 1))[0]
+        assert _relerr(got[b], want) <= ATTN_TOL
+
+
+def test_decode_append_uniform_position():
+    import torch
+    import aila_amd
+    B, Hq, Hkv, D, max_seq, p = 2, 8, 8, 128, 300, 299
+    q = dg.normal_bf16(4300, 0, (B, Hq, D))
+    kc = dg.normal_bf16(4300, 1, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(4300, 2, (B, Hkv, max_seq, D))
+    kn = dg.normal_bf16(4300, 3, (B, Hkv, D))
+    vn = dg.normal_bf16(4300, 4, (B, Hkv, D))
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out = aila_amd.gqa_decode_append(_t(q), _t(kn), _t(vn), _t(kc), _t(vc), p, workspace=ws)
+    torch.cuda.synchronize()
+    kc[:, :, p] = kn
+    vc[:, :, p] = vn
+    want = dg.bf16_to_f32(oracle.attention_decode_baseline(q, kc, vc, B, Hq, Hkv, D, max_seq, p + 1))
+    assert _relerr(dg.bf16_to_f32(_np_bf16(out)), want) <= ATTN_TOL

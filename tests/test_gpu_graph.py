@@ -1,5 +1,5 @@
-"""HIP-graph replay of a decode step (kv_append + split-K GQA decode with
-device-side lengths + DeltaNet decode + length advance) matches the same
+"""HIP-graph replay of a decode step (fused K/V append + split-K GQA decode
+with device-side positions + DeltaNet decode + position advance) matches the same
 step run eagerly, replay after replay, with eager work and synchronisation
 between the replays."""
 import numpy as np
@@ -33,8 +33,8 @@ def test_graph_replay_matches_eager():
                     o=torch.empty((B, Hq, D), **bf), do=torch.empty((B, Hv, d), **bf))
 
     def step(S, x):
-        aila_amd.kv_append(x["kn"], x["vn"], S["kc"], S["vc"], positions=S["pos"])
-        aila_amd.gqa_decode(x["q"], S["kc"], S["vc"], max_seq, out=S["o"], workspace=ws, seq_lens=S["lens"])
+        aila_amd.gqa_decode_append(x["q"], x["kn"], x["vn"], S["kc"], S["vc"], max_seq - 1, out=S["o"],
+                                   workspace=ws, positions=S["pos"])
         aila_amd.deltanet_decode(x["dq"], x["dk"], x["dv"], x["da"], x["db"], S["st"], out=S["do"])
         S["pos"].add_(1)
         S["lens"].add_(1)
