@@ -175,8 +175,9 @@ def bench_config5(torch, aila_amd, steps, warmup):
 
 def roofline_gqa(torch, aila_amd, W, reps=64):
     """Dominant kernel: one GQA decode launch (split + merge dispatch) on a
-    config-5 layer at L = 32768, HIP events around each launch on the stream
-    the kernels run on (torch's current stream)."""
+    config-5 layer at L = 32768, timed with HIP events around a batch of
+    back-to-back launches on the stream the kernels run on (torch's current
+    stream)."""
     L = L5
     lens = torch.full((B5,), L, dtype=torch.int32, device="cuda")
     x = W["pool"][0][3]
@@ -185,14 +186,18 @@ def roofline_gqa(torch, aila_amd, W, reps=64):
     for _ in range(5):
         fn()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for s, e in evs:
-        s.record()
+    # One event pair around `reps` back-to-back launches (an event pair per
+    # launch adds its own gap to every measured interval). A spin kernel
+    # queued first keeps the device busy while the host enqueues, so the
+    # interval holds device work only.
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.4e9 * 0.02))   # ~20 ms at 2.4 GHz
+    s.record()
+    for _ in range(reps):
         fn()
-        e.record()
+    e.record()
     torch.cuda.synchronize()
-    durs = [s.elapsed_time(e) for s, e in evs]
-    avg_ms = statistics.mean(durs)
+    avg_ms = s.elapsed_time(e) / reps
     byts = gqa_bytes(B5, GQA_HQ, GQA_HKV, GQA_D, L)
     achieved = byts / (avg_ms * 1e-3) / 1e9
     traffic = None
