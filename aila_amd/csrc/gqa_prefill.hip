@@ -99,8 +99,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   __shared__ __attribute__((aligned(1024))) unsigned char sV0[2][C::TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char sV1[2][C::TILE];
 
-  const int grp = threadIdx.x / kThreads;               // 0 = A, 1 = B
-  const int t = threadIdx.x % kThreads, lane = t & 63, wave = t >> 6;
+  const int grp = __builtin_amdgcn_readfirstlane(threadIdx.x / kThreads);   // 0 = A, 1 = B
+  const int t = threadIdx.x % kThreads, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int m16 = lane & 15, g4 = lane >> 4;
   auto tileK = [&](int buf) __attribute__((always_inline)) -> unsigned char* { return buf ? sK1[grp] : sK0[grp]; };
   auto tileV = [&](int buf) __attribute__((always_inline)) -> unsigned char* { return buf ? sV1[grp] : sV0[grp]; };
@@ -132,18 +133,42 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   const bool cache_head = (k_cache != nullptr) && (h % G == 0);
 
   // ---- K/V block -> LDS by DMA (wave-contiguous KiB per instruction) ------
+  // Per-lane element offsets of the DMA sources relative to the block's first
+  // key row, fixed for the whole kernel; a block then only adds a uniform
+  // base. The last block of a ragged length clamps its rows instead.
+  // (Fixed extent: an array sized by C::LOADS and captured by the lambdas
+  // below makes the host pass drop the kernel's launch stub.)
+  static_assert(C::LOADS <= 8, "dma_off extent");
+  int dma_off[8];
+#pragma unroll
+  for (int i = 0; i < C::LOADS; ++i) {
+    const int p = (i * kWaves + wave) * 64 + lane;
+    const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
+    dma_off[i] = r * kv_row_stride + qc * 8;
+  }
   auto issue = [&](int buf, int kb) __attribute__((always_inline)) {
     const int key0 = kb * BN;
     unsigned char* tk = tileK(buf);
     unsigned char* tv = tileV(buf);
+    if (key0 + BN <= kv_len) {
+      const bf16* kb0 = Kh + static_cast<size_t>(key0) * kv_row_stride;
+      const bf16* vb0 = Vh + static_cast<size_t>(key0) * kv_row_stride;
 #pragma unroll
-    for (int i = 0; i < C::LOADS; ++i) {
-      const int wchunk = (i * kWaves + wave) * 64;     // first 16-byte slot of this wave instruction
-      const int p = wchunk + lane;
-      const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
-      const size_t goff = static_cast<size_t>(min(key0 + r, kv_len - 1)) * kv_row_stride + qc * 8;
-      __builtin_amdgcn_global_load_lds(Kh + goff, (lds_void_t*)(tk + wchunk * 16), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(Vh + goff, (lds_void_t*)(tv + wchunk * 16), 16, 0, 0);
+      for (int i = 0; i < C::LOADS; ++i) {
+        const int wchunk = (i * kWaves + wave) * 64;
+        __builtin_amdgcn_global_load_lds(kb0 + dma_off[i], (lds_void_t*)(tk + wchunk * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb0 + dma_off[i], (lds_void_t*)(tv + wchunk * 16), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::LOADS; ++i) {
+        const int wchunk = (i * kWaves + wave) * 64;     // first 16-byte slot of this wave instruction
+        const int p = wchunk + lane;
+        const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
+        const size_t goff = static_cast<size_t>(min(key0 + r, kv_len - 1)) * kv_row_stride + qc * 8;
+        __builtin_amdgcn_global_load_lds(Kh + goff, (lds_void_t*)(tk + wchunk * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(Vh + goff, (lds_void_t*)(tv + wchunk * 16), 16, 0, 0);
+      }
     }
   };
   // The chunk's own key rows of query block qb go to the cache (fused
@@ -256,56 +281,64 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
         va[dt] = as_bf16x8(w);
       }
     };
-    // mask (raw scores) and row maxima
-    const bool need_mask = (key0 + BN - 1 > wave_qmin);
+    // Mask (raw scores), row maxima and P^T operands. The masked variant is
+    // only instantiated for blocks that reach the diagonal (a wave-uniform
+    // branch; a select per element would cost every block).
     float alpha[C::QT];
     bool any_rescale = false;
-#pragma unroll
-    for (int qt = 0; qt < C::QT; ++qt) {
-      const int qpos = wave_qmin + qt * 16 + m16;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (need_mask && (key0 + kt * 16 + g4 * 4 + j > qpos)) st[kt][qt][j] = -INFINITY;
-          mx = fmaxf(mx, st[kt][qt][j]);
-        }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      mx *= scale_log2;
-      // Lazy rescaling: the reference max only moves when the block max
-      // exceeds it by more than 2^8 (p <= 256 stays exact in fp32 and bf16
-      // range); the normalisation by l is unaffected.
-      const bool grow = mx > m_run[qt] + kLazyRescaleLog2;
-      const float mn = grow ? mx : m_run[qt];
-      alpha[qt] = grow ? ((m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn)) : 1.0f;
-      m_run[qt] = mn;
-      any_rescale |= grow;
-    }
-    // P^T operands: step s2 covers keys 32*s2 + {4g..4g+3, 16+4g..16+4g+3}
-    bf16x8_t pb[C::PS][C::QT];
+    bf16x8_t pb[C::PS][C::QT];   // step s2 covers keys 32*s2 + {4g..4g+3, 16+4g..16+4g+3}
     float l_psum[C::QT];
+    auto softmax = [&](const bool masked) __attribute__((always_inline)) {
+      if (masked) {
 #pragma unroll
-    for (int qt = 0; qt < C::QT; ++qt) {
-      l_psum[qt] = 0.f;
-      const float nm = -m_run[qt];
+        for (int qt = 0; qt < C::QT; ++qt) {
+          const int rel = wave_qmin + qt * 16 + m16 - key0 - g4 * 4;   // key offset limit
 #pragma unroll
-      for (int s2 = 0; s2 < C::PS; ++s2) {
-        float p[8];
+          for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
-          p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
+            for (int j = 0; j < 4; ++j)
+              if (kt * 16 + j > rel) st[kt][qt][j] = -INFINITY;
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) l_psum[qt] += p[j];
-        const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                         pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
-        pb[s2][qt] = as_bf16x8(w);
       }
-    }
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mx = fmaxf(mx, st[kt][qt][j]);
+        mx = xrow4_max(mx) * scale_log2;
+        // Lazy rescaling: the reference max only moves when the block max
+        // exceeds it by more than 2^8 (p <= 256 stays exact in fp32 and bf16
+        // range); the normalisation by l is unaffected.
+        const bool grow = mx > m_run[qt] + kLazyRescaleLog2;
+        const float mn = grow ? mx : m_run[qt];
+        alpha[qt] = grow ? ((m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn)) : 1.0f;
+        m_run[qt] = mn;
+        any_rescale |= grow;
+      }
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) {
+        l_psum[qt] = 0.f;
+        const float nm = -m_run[qt];
+#pragma unroll
+        for (int s2 = 0; s2 < C::PS; ++s2) {
+          float p[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
+            p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) l_psum[qt] += p[j];
+          const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                           pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
+          pb[s2][qt] = as_bf16x8(w);
+        }
+      }
+    };
+    if (key0 + BN - 1 > wave_qmin) softmax(true);
+    else softmax(false);
     if (__any(any_rescale)) {
 #pragma unroll
       for (int qt = 0; qt < C::QT; ++qt) {
