@@ -55,6 +55,11 @@ def build(verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # Load check: a kernel template whose host-side launch stub was not
+    # emitted leaves an undefined symbol that only shows at dlopen.
+    r = subprocess.run([sys.executable, "-c", f"import ctypes; ctypes.CDLL({LIB!r})"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{LIB} does not load:\n{r.stderr.strip().splitlines()[-1]}")
     # C++ ops:: layer over the C ABI (host code only)
     host_srcs = sorted(glob.glob(os.path.join(HOST, "*.cpp")))
     cmd = [HIPCC, "-std=c++17", "-O2", "-fPIC", "-shared", "-I", HOST, "-I", os.path.join(ROOT, "include"),

@@ -32,9 +32,10 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLazyRescaleLog2 = 8.0f;
+constexpr int kPrefetch = 4;   // LDS operand reads in flight ahead of their MFMAs
 constexpr int kNumXcd = 8;   // MI355X: 8 accelerator complex dies, one L2 each
-// s_waitcnt immediate (gfx9 encoding): vmcnt = 0, expcnt and lgkmcnt not waited on.
-constexpr int kWaitVmcntZero = 0x0F70;
+// Buffer resource word 3 for raw (untyped, unswizzled) gfx9 buffer loads.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 template <int D, int RPW, int BN>
 struct PrefillCfg {
@@ -58,33 +59,94 @@ struct PrefillCfg {
 
 // 16-byte chunk swizzle of K/V tile rows. Tiles are written by direct
 // global->LDS loads (one contiguous KiB per wave instruction, so rows cannot
-// be padded); the XOR keeps both read patterns conflict-free: the S^T A
-// operand (16 rows x one 16-byte chunk) and the transposed V reads (8 rows x
-// one 32-byte chunk pair per half wave).
+// be padded); the XOR keeps both read patterns free of bank conflicts on the
+// 32 four-byte banks (128 B per clock):
+//  - S^T A operand (ds_read_b128): 8 consecutive rows, one chunk each, per
+//    clock -> the low three bits of swz must differ over any 8 aligned rows;
+//  - transposed V (ds_read_b64_tr_b16): 4 consecutive rows x one 32-byte
+//    chunk pair per clock -> bits 1..2 must differ over any 4 aligned rows.
+// swz = (r&3)<<1 | (r>>2)&1 is a bit permutation meeting both; rows 8..15
+// additionally flip bit 3 where a row has 16 or more chunks.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);        // 8 chunks per row
+  const int lo = ((r & 3) << 1) | ((r >> 2) & 1);
+  if constexpr (D >= 128) return lo | (r & 8);
+  else return lo;                                   // 8 chunks per row
 }
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// Workgroup barrier that orders LDS accesses only (no wait for outstanding
+// global loads or LDS DMAs).
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Raw buffer resource (gfx9 layout): 48-bit base, stride 0, num_records in
+// bytes, word 3 = untyped raw access. Loads past num_records return zeros.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, int num_bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu,
+               static_cast<uint32_t>(num_bytes), static_cast<uint32_t>(kBufferRsrcWord3)};
+}
+
+// One wave-wide 16-byte-per-lane buffer load written straight to LDS: lane l
+// lands at lds + 16*l (the wave's KiB is contiguous). Issued as inline asm so
+// the compiler does not treat the LDS tiles as pending DMA targets (it would
+// wait for every DMA in flight before any LDS read); the kernel orders these
+// writes itself with counted vmcnt waits and barriers.
+__device__ __forceinline__ void dma16_to_lds_at(const u32x4& rsrc, int voffset, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(m0)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_to_lds(const u32x4& rsrc, int voffset, void* lds) {
+  dma16_to_lds_at(rsrc, voffset, static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most N vector
+// memory operations of this wave are outstanding; expcnt and lgkmcnt are
+// left at their maxima (not waited on).
+template <int N>
+constexpr int vmcnt_imm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  return (N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
 
 // One workgroup = two 4-wave groups and one head. It owns a balanced pair of
 // query blocks: light block i and heavy block n-1-i (causal work grows with
 // the block index, so every pair costs n+1 key blocks when start_pos = 0).
 // Group A walks the light block's keys and then the first part of the heavy
-// block's keys; group B walks the rest of the heavy block's keys; both run
-// the same number of iterations (within one), each on its own double-buffered
+// block's keys; group B walks the rest of the heavy block's keys; both walk
+// the same number of key blocks (within one), each on its own double-buffered
 // K/V tiles, and the heavy block's two partial softmax states are merged
 // through LDS at the end.
 //
-// K and V tiles are row-major [BN][D] in LDS, filled by global_load_lds
-// (no staging registers). O^T += V^T P^T takes its V^T operand from
-// ds_read_b64_tr_b16: within a 16-lane group, lane i addresses 4 bf16 of
-// row kbase + i/4 at column d0 + 4*(i%4), and lane j receives V[kbase+r][d0+j]
-// for r = 0..3 - four keys of one head dim, the A-operand layout.
+// Schedule (ping-pong). A group alternates a matrix phase M(j) - O^T +=
+// V_{j-1}^T P_{j-1}^T, then S_j^T = K_j Q^T - with a vector phase V(j) - the
+// softmax of S_j into P_j. Group B runs one phase behind group A, with a
+// workgroup barrier between phases, so on every SIMD one wave feeds the
+// matrix core and reads LDS while the other runs the softmax on the vector
+// ALU (the two overlap across waves, not within one wave).
+//
+// Tiles: M(j) reads K_j from Kbuf[j%2] and V_{j-1} from Vbuf[(j-1)%2]. When
+// M(j) is done, V(j) refills exactly those two buffers by DMA with V_{j+1}
+// and K_{j+2}, which M(j+1) and M(j+2) need three phases later; before
+// M(j+1) each wave waits for its DMAs of V(j-1) only. The phase loop is
+// unrolled by two so every LDS access names its buffer at compile time and
+// the compiler can tell reads apart from the DMAs still in flight.
+//
+// K and V tiles are row-major [BN][D] in LDS (swizzled 16-byte chunks).
+// O^T += V^T P^T takes its V^T operand from ds_read_b64_tr_b16: within a
+// 16-lane group, lane i addresses 4 bf16 of row kbase + i/4 at column
+// d0 + 4*(i%4), and lane j receives V[kbase+r][d0+j] for r = 0..3 - four
+// keys of one head dim, the A-operand layout.
 template <int D, int RPW, int BN>
 __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     const bf16* __restrict__ q, int q_row_stride, const bf16* __restrict__ k,
@@ -103,8 +165,6 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   const int t = threadIdx.x % kThreads, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int m16 = lane & 15, g4 = lane >> 4;
-  auto tileK = [&](int buf) __attribute__((always_inline)) -> unsigned char* { return buf ? sK1[grp] : sK0[grp]; };
-  auto tileV = [&](int buf) __attribute__((always_inline)) -> unsigned char* { return buf ? sV1[grp] : sV0[grp]; };
 
   const int nqb = (S + C::BM - 1) / C::BM;
   const int npair = (nqb + 1) / 2;
@@ -122,7 +182,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   auto nkeyblk = [&](int qb) __attribute__((always_inline)) { return (start_pos + min((qb + 1) * C::BM, S) - 1) / BN + 1; };
   const int nl = (ql < qh) ? nkeyblk(ql) : 0;           // a middle block pairs with itself
   const int nh = nkeyblk(qh);
-  const int tA = (nl + nh + 1) / 2, tB = nl + nh - tA;
+  const int tA = (nl + nh + 1) / 2, tB = nl + nh - tA;   // tA >= tB
   const int hsplit = tA - nl;                           // heavy key blocks walked by A
   const int my_n = grp == 0 ? tA : tB;
   auto kb_of = [&](int it) __attribute__((always_inline)) { return grp == 0 ? (it < nl ? it : it - nl) : hsplit + it; };
@@ -130,12 +190,12 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   const int kv_len = start_pos + S;
   const bf16* Kh = k + kvh * kv_head_stride;
   const bf16* Vh = v + kvh * kv_head_stride;
-  const bool cache_head = (k_cache != nullptr) && (h % G == 0);
 
   // ---- K/V block -> LDS by DMA (wave-contiguous KiB per instruction) ------
-  // Per-lane element offsets of the DMA sources relative to the block's first
-  // key row, fixed for the whole kernel; a block then only adds a uniform
-  // base. The last block of a ragged length clamps its rows instead.
+  // Buffer loads straight into LDS. The buffer resource of a block starts at
+  // its first key row and ends at the last valid row (kv_len), so rows past
+  // a ragged end read as zeros (those keys are causally masked) and every
+  // lane's byte offset is a constant of the kernel.
   // (Fixed extent: an array sized by C::LOADS and captured by the lambdas
   // below makes the host pass drop the kernel's launch stub.)
   static_assert(C::LOADS <= 8, "dma_off extent");
@@ -144,52 +204,14 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   for (int i = 0; i < C::LOADS; ++i) {
     const int p = (i * kWaves + wave) * 64 + lane;
     const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
-    dma_off[i] = r * kv_row_stride + qc * 8;
+    dma_off[i] = (r * kv_row_stride + qc * 8) * 2;
   }
-  auto issue = [&](int buf, int kb) __attribute__((always_inline)) {
+  auto issue_tile = [&](unsigned char* tile, const bf16* base, int kb) __attribute__((always_inline)) {
     const int key0 = kb * BN;
-    unsigned char* tk = tileK(buf);
-    unsigned char* tv = tileV(buf);
-    if (key0 + BN <= kv_len) {
-      const bf16* kb0 = Kh + static_cast<size_t>(key0) * kv_row_stride;
-      const bf16* vb0 = Vh + static_cast<size_t>(key0) * kv_row_stride;
+    const u32x4 src = buffer_rsrc(base + static_cast<size_t>(key0) * kv_row_stride,
+                                  (kv_len - key0) * kv_row_stride * 2);
 #pragma unroll
-      for (int i = 0; i < C::LOADS; ++i) {
-        const int wchunk = (i * kWaves + wave) * 64;
-        __builtin_amdgcn_global_load_lds(kb0 + dma_off[i], (lds_void_t*)(tk + wchunk * 16), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vb0 + dma_off[i], (lds_void_t*)(tv + wchunk * 16), 16, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < C::LOADS; ++i) {
-        const int wchunk = (i * kWaves + wave) * 64;     // first 16-byte slot of this wave instruction
-        const int p = wchunk + lane;
-        const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
-        const size_t goff = static_cast<size_t>(min(key0 + r, kv_len - 1)) * kv_row_stride + qc * 8;
-        __builtin_amdgcn_global_load_lds(Kh + goff, (lds_void_t*)(tk + wchunk * 16), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(Vh + goff, (lds_void_t*)(tv + wchunk * 16), 16, 0, 0);
-      }
-    }
-  };
-  // The chunk's own key rows of query block qb go to the cache (fused
-  // copy_to_cache), copied out of the LDS tiles.
-  auto write_cache = [&](int buf, int kb, int qb) __attribute__((always_inline)) {
-    const int key0 = kb * BN;
-    const int cq0 = qb * C::BM, cq1 = min(cq0 + C::BM, S) - 1;
-    if (!(cache_head && key0 + BN - 1 >= cq0 && key0 <= cq1)) return;
-    const unsigned char* tk = tileK(buf);
-    const unsigned char* tv = tileV(buf);
-#pragma unroll
-    for (int i = 0; i < C::LOADS; ++i) {
-      const int p = i * kThreads + t;
-      const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
-      const int key = key0 + r;
-      if (key >= cq0 && key <= cq1) {
-        const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + key) * D + qc * 8;
-        *reinterpret_cast<u32x4*>(k_cache + dst) = *reinterpret_cast<const u32x4*>(tk + p * 16);
-        *reinterpret_cast<u32x4*>(v_cache + dst) = *reinterpret_cast<const u32x4*>(tv + p * 16);
-      }
-    }
+    for (int i = 0; i < C::LOADS; ++i) dma16_to_lds(src, dma_off[i], tile + (i * kWaves + wave) * 64 * 16);
   };
 
   // ---- per-segment state ---------------------------------------------------
@@ -214,10 +236,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   auto store_segment = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int qt = 0; qt < C::QT; ++qt) {
-      float l = l_run[qt];
-      l += __shfl_xor(l, 16);
-      l += __shfl_xor(l, 32);
-      const float inv = 1.0f / l;
+      const float inv = 1.0f / l_run[qt];   // full row sum, held by every lane
       const int row = seg_qb * C::BM + wave * RPW + qt * 16 + m16;
       if (row < S) {
         bf16* orow = out + static_cast<size_t>(row) * o_row_stride + h * D + g4 * 4;
@@ -231,114 +250,94 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     }
   };
 
-  // ---- one key block against the current segment ---------------------------
-  auto compute_block = [&](int buf, int kb) __attribute__((always_inline)) {
+  // ---- S^T = K Q^T for one key block (matrix phase) -----------------------
+  f32x4 st[C::KT][C::QT];
+  bool s_valid = false, p_valid = false;
+  int s_kb = 0;
+  auto s_block = [&](const unsigned char* tk, int kb) __attribute__((always_inline)) {
     const int key0 = kb * BN;
     const int wave_qmin = start_pos + seg_qb * C::BM + wave * RPW;
-    if (key0 > wave_qmin + RPW - 1) return;   // every key of the block is in this wave's future
-    const unsigned char* tk = tileK(buf);
-    const unsigned char* tv = tileV(buf);
-    // S^T = K Q^T; the K operands of k-step ks+1 are read while the MFMAs of
-    // step ks run.
-    auto load_k = [&](int ks, bf16x8_t* ka) __attribute__((always_inline)) {
-#pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt) {
-        const int r = kt * 16 + m16;
-        ka[kt] = as_bf16x8(*reinterpret_cast<const u32x4*>(tk + r * C::RB + (((ks * 4 + g4) ^ swz<D>(r)) << 4)));
-      }
+    s_kb = kb;
+    s_valid = key0 <= wave_qmin + RPW - 1;   // otherwise every key is in this wave's future
+    if (!s_valid) return;
+    // K operands in (ks, kt) order, each read kPrefetch operands ahead of the
+    // MFMAs that use it; the schedule barriers keep that distance (left
+    // alone, the scheduler issues each read just two MFMAs before its use).
+    auto load_k = [&](int i) __attribute__((always_inline)) {
+      const int ks = i / C::KT, kt = i % C::KT;
+      const int r = kt * 16 + m16;
+      return as_bf16x8(*reinterpret_cast<const u32x4*>(tk + r * C::RB + (((ks * 4 + g4) ^ swz<D>(r)) << 4)));
     };
-    f32x4 st[C::KT][C::QT];
 #pragma unroll
     for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
       for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    bf16x8_t ka0[C::KT], ka1[C::KT];
-    load_k(0, ka0);
+    constexpr int NK = C::KS * C::KT;
+    bf16x8_t kop[NK];
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
-      bf16x8_t* cur = (ks & 1) ? ka1 : ka0;
-      bf16x8_t* nxt = (ks & 1) ? ka0 : ka1;
-      if (ks + 1 < C::KS) load_k(ks + 1, nxt);
+    for (int i = 0; i < kPrefetch && i < NK; ++i) kop[i] = load_k(i);
 #pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt)
+    for (int i = 0; i < NK; ++i) {
+      if (i + kPrefetch < NK) kop[i + kPrefetch] = load_k(i + kPrefetch);
+      const int ks = i / C::KT, kt = i % C::KT;
 #pragma unroll
-        for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = mfma16x16x32(cur[kt], qb_op[qt][ks], st[kt][qt]);
+      for (int qt = 0; qt < C::QT; ++qt) st[kt][qt] = mfma16x16x32(kop[i], qb_op[qt][ks], st[kt][qt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // V^T operands come from transposing LDS reads.
-    const int vr = 4 * g4 + (m16 >> 2);          // row within a 32-key step (first half)
-    const int vc = 4 * (m16 & 3);                // column offset within a 16-wide d tile
-    auto load_v = [&](int s2, bf16x8_t* va) __attribute__((always_inline)) {
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) {
-        const int d = dt * 16 + vc;
-        const int r0 = s2 * 32 + vr, r1 = r0 + 16;
-        const unsigned char* p0 = tv + r0 * C::RB + (((d >> 3) ^ swz<D>(r0)) << 4) + ((d & 7) << 1);
-        const unsigned char* p1 = tv + r1 * C::RB + (((d >> 3) ^ swz<D>(r1)) << 4) + ((d & 7) << 1);
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p0);
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p1);
-        const u32x4 w = {__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
-                         __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]};
-        va[dt] = as_bf16x8(w);
-      }
-    };
-    // Mask (raw scores), row maxima and P^T operands. The masked variant is
-    // only instantiated for blocks that reach the diagonal (a wave-uniform
-    // branch; a select per element would cost every block).
-    float alpha[C::QT];
-    bool any_rescale = false;
-    bf16x8_t pb[C::PS][C::QT];   // step s2 covers keys 32*s2 + {4g..4g+3, 16+4g..16+4g+3}
-    float l_psum[C::QT];
-    auto softmax = [&](const bool masked) __attribute__((always_inline)) {
-      if (masked) {
-#pragma unroll
-        for (int qt = 0; qt < C::QT; ++qt) {
-          const int rel = wave_qmin + qt * 16 + m16 - key0 - g4 * 4;   // key offset limit
-#pragma unroll
-          for (int kt = 0; kt < C::KT; ++kt)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (kt * 16 + j > rel) st[kt][qt][j] = -INFINITY;
-        }
-      }
+  };
+
+  // ---- softmax of S_j into P_j (vector phase) -------------------------------
+  bf16x8_t pb[C::PS][C::QT];   // step s2 covers keys 32*s2 + {4g..4g+3, 16+4g..16+4g+3}
+  auto softmax = [&](const bool masked) __attribute__((always_inline)) {
+    const int key0 = s_kb * BN;
+    const int wave_qmin = start_pos + seg_qb * C::BM + wave * RPW;
+    if (masked) {
 #pragma unroll
       for (int qt = 0; qt < C::QT; ++qt) {
-        float mx = -INFINITY;
+        const int rel = wave_qmin + qt * 16 + m16 - key0 - g4 * 4;   // key offset limit
 #pragma unroll
         for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) mx = fmaxf(mx, st[kt][qt][j]);
-        mx = xrow4_max(mx) * scale_log2;
-        // Lazy rescaling: the reference max only moves when the block max
-        // exceeds it by more than 2^8 (p <= 256 stays exact in fp32 and bf16
-        // range); the normalisation by l is unaffected.
-        const bool grow = mx > m_run[qt] + kLazyRescaleLog2;
-        const float mn = grow ? mx : m_run[qt];
-        alpha[qt] = grow ? ((m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn)) : 1.0f;
-        m_run[qt] = mn;
-        any_rescale |= grow;
+          for (int j = 0; j < 4; ++j)
+            if (kt * 16 + j > rel) st[kt][qt][j] = -INFINITY;
       }
+    }
+    float alpha[C::QT];
+    bool any_rescale = false;
 #pragma unroll
-      for (int qt = 0; qt < C::QT; ++qt) {
-        l_psum[qt] = 0.f;
-        const float nm = -m_run[qt];
+    for (int qt = 0; qt < C::QT; ++qt) {
+      float mx = -INFINITY;
 #pragma unroll
-        for (int s2 = 0; s2 < C::PS; ++s2) {
-          float p[8];
+      for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
-            p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
-          }
+        for (int j = 0; j < 4; ++j) mx = fmaxf(mx, st[kt][qt][j]);
+      mx = xrow4_max(mx) * scale_log2;
+      // Lazy rescaling: the reference max only moves when the block max
+      // exceeds it by more than 2^8 (p <= 256 stays exact in fp32 and bf16
+      // range); the normalisation by l is unaffected.
+      const bool grow = mx > m_run[qt] + kLazyRescaleLog2;
+      const float mn = grow ? mx : m_run[qt];
+      alpha[qt] = grow ? ((m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn)) : 1.0f;
+      m_run[qt] = mn;
+      any_rescale |= grow;
+    }
 #pragma unroll
-          for (int j = 0; j < 8; ++j) l_psum[qt] += p[j];
-          const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                           pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
-          pb[s2][qt] = as_bf16x8(w);
+    for (int qt = 0; qt < C::QT; ++qt) {
+      const float nm = -m_run[qt];
+#pragma unroll
+      for (int s2 = 0; s2 < C::PS; ++s2) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
+          p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
         }
+        const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                         pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
+        pb[s2][qt] = as_bf16x8(w);
       }
-    };
-    if (key0 + BN - 1 > wave_qmin) softmax(true);
-    else softmax(false);
+    }
+    // o_acc and l hold every block before j (M(j) added P_{j-1}).
     if (__any(any_rescale)) {
 #pragma unroll
       for (int qt = 0; qt < C::QT; ++qt) {
@@ -347,52 +346,114 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
         for (int dt = 0; dt < C::DT; ++dt) o_acc[dt][qt] *= alpha[qt];
       }
     }
+  };
+
+  // ---- O^T += V^T P^T and l += rowsum(P) (matrix phase) ---------------------
+  auto pv_block = [&](const unsigned char* tv) __attribute__((always_inline)) {
+    // V^T operands come from transposing LDS reads, in (s2, dt) order, each
+    // read kPrefetch operands ahead of its MFMAs (as the K operands above).
+    const int vr = 4 * g4 + (m16 >> 2);          // row within a 32-key step (first half)
+    const int vc = 4 * (m16 & 3);                // column offset within a 16-wide d tile
+    auto load_v = [&](int i) __attribute__((always_inline)) {
+      const int s2 = i / C::DT, dt = i % C::DT;
+      const int d = dt * 16 + vc;
+      const int r0 = s2 * 32 + vr, r1 = r0 + 16;
+      const unsigned char* p0 = tv + r0 * C::RB + (((d >> 3) ^ swz<D>(r0)) << 4) + ((d & 7) << 1);
+      const unsigned char* p1 = tv + r1 * C::RB + (((d >> 3) ^ swz<D>(r1)) << 4) + ((d & 7) << 1);
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p0);
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p1);
+      const u32x4 w = {__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
+                       __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]};
+      return as_bf16x8(w);
+    };
+    constexpr int NV = C::PS * C::DT;
+    bf16x8_t vop[NV];
 #pragma unroll
-    for (int qt = 0; qt < C::QT; ++qt) l_run[qt] += l_psum[qt];
-    // O^T += V^T P^T, one 32-key step at a time.
+    for (int i = 0; i < kPrefetch && i < NV; ++i) vop[i] = load_v(i);
+    // Row sums of P on the matrix cores while the first reads are in flight:
+    // a ones A operand gives every output row the column sums of P^T, i.e.
+    // the full row sum of each query (all 32 keys of the step, the bf16 P the
+    // numerator uses) in every lane.
+    {
+      const u32x4 ones_w = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+      const bf16x8_t ones = as_bf16x8(ones_w);
 #pragma unroll
-    for (int s2 = 0; s2 < C::PS; ++s2) {
-      bf16x8_t va[C::DT];
-      load_v(s2, va);
+      for (int qt = 0; qt < C::QT; ++qt) {
+        f32x4 ls = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt)
+        for (int s2 = 0; s2 < C::PS; ++s2) ls = mfma16x16x32(ones, pb[s2][qt], ls);
+        l_run[qt] += ls[0];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int qt = 0; qt < C::QT; ++qt) o_acc[dt][qt] = mfma16x16x32(va[dt], pb[s2][qt], o_acc[dt][qt]);
+    for (int i = 0; i < NV; ++i) {
+      if (i + kPrefetch < NV) vop[i + kPrefetch] = load_v(i + kPrefetch);
+      const int s2 = i / C::DT, dt = i % C::DT;
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) o_acc[dt][qt] = mfma16x16x32(vop[i], pb[s2][qt], o_acc[dt][qt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // ---- main loop: both groups in lock step -----------------------------------
+  // ---- prologue: K_0, V_0, K_1 -------------------------------------------
   if (my_n > 0) {
     begin_segment(qb_of(0));
-    issue(0, kb_of(0));
+    issue_tile(sK0[grp], Kh, kb_of(0));
+    issue_tile(sV0[grp], Vh, kb_of(0));
+    if (my_n > 1) issue_tile(sK1[grp], Kh, kb_of(1));
   }
-  __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   __syncthreads();
-  auto iteration = [&](int cur, int nxt, int it) __attribute__((always_inline)) {
-    if (it + 1 < my_n) issue(nxt, kb_of(it + 1));
-    if (it < my_n) {
-      if (cache_head) write_cache(cur, kb_of(it), qb_of(it));
-      compute_block(cur, kb_of(it));
+
+  // One block step: matrix phase M(j), barrier, vector phase V(j), barrier.
+  // The phase barriers fence LDS only: inside the loop LDS is written only by
+  // the DMAs, whose completion the explicit vmcnt waits establish (a full
+  // __syncthreads would wait for every DMA still in flight).
+  // kcur = Kbuf[j%2] (K_j, then refilled with K_{j+2}); vprev = Vbuf[(j+1)%2]
+  // (V_{j-1}, then refilled with V_{j+1}).
+  const int nsteps = tA;   // both groups run tA steps; B's last is empty when tB < tA
+  auto step = [&](int j, unsigned char* kcur, unsigned char* vprev) __attribute__((always_inline)) {
+    // M(j)
+    if (j >= 1 && j - 1 < my_n && p_valid) pv_block(vprev);
+    if (j < my_n) {
+      if (j >= 1 && qb_of(j) != qb_of(j - 1)) {   // group A moves from its light to its heavy block
+        store_segment();
+        begin_segment(qb_of(j));
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+      }
+      s_block(kcur, kb_of(j));
+    } else {
+      s_valid = false;
     }
-    __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);   // the DMA into the other buffer has landed
-    __syncthreads();
-  };
-  auto run = [&](int it0, int it1) __attribute__((always_inline)) {
-    for (int it = it0; it < it1; ++it) iteration(it & 1, (it + 1) & 1, it);
-  };
-  // Two loops split at the light/heavy switch of group A, so no loop body
-  // holds a Q reload.
-  const int it_switch = (nl > 0 && hsplit > 0) ? nl : tA;
-  run(0, it_switch);
-  if (it_switch < tA) {
-    if (grp == 0) {
-      store_segment();
-      begin_segment(qh);
+    phase_barrier();
+    if (j >= nsteps) return;
+    // V(j)
+    const bool nv = j + 1 < my_n, nk = j + 2 < my_n;
+    if (nv) issue_tile(vprev, Vh, kb_of(j + 1));
+    if (nk) issue_tile(kcur, Kh, kb_of(j + 2));
+    p_valid = s_valid;
+    if (s_valid) {
+      if (s_kb * BN + BN - 1 > start_pos + seg_qb * C::BM + wave * RPW) softmax(true);
+      else softmax(false);
     }
-    run(it_switch, tA);
+    // M(j+1) needs K_{j+1} and V_j, issued in V(j-1): only this phase's DMAs
+    // may stay in flight.
+    if (nk) __builtin_amdgcn_s_waitcnt(vmcnt_imm<2 * C::LOADS>());
+    else if (nv) __builtin_amdgcn_s_waitcnt(vmcnt_imm<C::LOADS>());
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    phase_barrier();
+  };
+  if (grp == 1) phase_barrier();   // group B runs one phase behind
+  for (int j = 0; j <= nsteps; j += 2) {
+    step(j, sK0[grp], sV1[grp]);
+    if (j + 1 <= nsteps) step(j + 1, sK1[grp], sV0[grp]);
   }
+  if (grp == 0) phase_barrier();
 
   // ---- finish: light block of A, heavy block (merged when split) -------------
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+  __syncthreads();
   const bool a_has_heavy = hsplit > 0;
   const bool b_has_heavy = tB > 0;
   if (grp == 0 && !a_has_heavy && nl > 0) store_segment();          // A only had the light block
@@ -445,6 +506,23 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     store_segment();
   } else if (b_has_heavy && grp == 1) {
     store_segment();
+  }
+
+  // ---- fused copy_to_cache: this pair's own K/V rows, one head per KV group --
+  if (k_cache != nullptr && h % G == 0) {
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+      const int qb = pass == 0 ? qh : ql;
+      if (pass == 1 && ql == qh) break;
+      const int r0 = qb * C::BM, r1 = min(r0 + C::BM, S);
+      for (int p = threadIdx.x; p < (r1 - r0) * C::NC; p += 2 * kThreads) {
+        const int row = r0 + p / C::NC, c = p % C::NC;
+        const size_t src = static_cast<size_t>(row) * kv_row_stride + c * 8;
+        const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + row) * D + c * 8;
+        *reinterpret_cast<u32x4*>(k_cache + dst) = ld16(Kh + src);
+        *reinterpret_cast<u32x4*>(v_cache + dst) = ld16(Vh + src);
+      }
+    }
   }
 }
 
