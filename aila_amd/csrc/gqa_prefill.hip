@@ -57,21 +57,23 @@ struct PrefillCfg {
   static_assert(kWaves * QT * 64 * 8 <= 2 * TILE, "m/l scratch fits in the buffer-0 V tiles");
 };
 
-// 16-byte chunk swizzle of K/V tile rows. Tiles are written by direct
-// global->LDS loads (one contiguous KiB per wave instruction, so rows cannot
-// be padded); the XOR keeps both read patterns free of bank conflicts on the
-// 32 four-byte banks (128 B per clock):
-//  - S^T A operand (ds_read_b128): 8 consecutive rows, one chunk each, per
-//    clock -> the low three bits of swz must differ over any 8 aligned rows;
-//  - transposed V (ds_read_b64_tr_b16): 4 consecutive rows x one 32-byte
-//    chunk pair per clock -> bits 1..2 must differ over any 4 aligned rows.
-// swz = (r&3)<<1 | (r>>2)&1 is a bit permutation meeting both; rows 8..15
-// additionally flip bit 3 where a row has 16 or more chunks.
+// 16-byte chunk swizzles of the K and V tile rows (XOR on the chunk index).
+// Tiles are written by DMA (one contiguous KiB per wave instruction, so rows
+// cannot be padded). Measured on gfx950 over all bit-permutation swizzles of
+// 256-byte rows: the S^T A-operand reads (ds_read_b128, 16 rows x one chunk
+// per 16 lanes) reach ~245 B/clk/CU only when bit 0 of the swizzle comes from
+// row bit 0 or 1 (else ~126), and the transposed V reads (ds_read_b64_tr_b16)
+// reach ~166 B/clk/CU only when it comes from row bit 3 (else ~123). The two
+// tiles are separate, so each gets its own.
 template <int D>
-__device__ __forceinline__ int swz(int r) {
-  const int lo = ((r & 3) << 1) | ((r >> 2) & 1);
-  if constexpr (D >= 128) return lo | (r & 8);
-  else return lo;                                   // 8 chunks per row
+__device__ __forceinline__ int swz_k(int r) {
+  if constexpr (D >= 128) return r & 15;
+  else return r & 7;                                 // 8 chunks per row
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
+  if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
 }
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -199,19 +201,20 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   // (Fixed extent: an array sized by C::LOADS and captured by the lambdas
   // below makes the host pass drop the kernel's launch stub.)
   static_assert(C::LOADS <= 8, "dma_off extent");
-  int dma_off[8];
+  int koff[8], voff[8];
 #pragma unroll
   for (int i = 0; i < C::LOADS; ++i) {
     const int p = (i * kWaves + wave) * 64 + lane;
-    const int r = p / C::NC, qc = (p % C::NC) ^ swz<D>(r);
-    dma_off[i] = (r * kv_row_stride + qc * 8) * 2;
+    const int r = p / C::NC;
+    koff[i] = (r * kv_row_stride + ((p % C::NC) ^ swz_k<D>(r)) * 8) * 2;
+    voff[i] = (r * kv_row_stride + ((p % C::NC) ^ swz_v<D>(r)) * 8) * 2;
   }
-  auto issue_tile = [&](unsigned char* tile, const bf16* base, int kb) __attribute__((always_inline)) {
+  auto issue_tile = [&](unsigned char* tile, const bf16* base, const int* off, int kb) __attribute__((always_inline)) {
     const int key0 = kb * BN;
     const u32x4 src = buffer_rsrc(base + static_cast<size_t>(key0) * kv_row_stride,
                                   (kv_len - key0) * kv_row_stride * 2);
 #pragma unroll
-    for (int i = 0; i < C::LOADS; ++i) dma16_to_lds(src, dma_off[i], tile + (i * kWaves + wave) * 64 * 16);
+    for (int i = 0; i < C::LOADS; ++i) dma16_to_lds(src, off[i], tile + (i * kWaves + wave) * 64 * 16);
   };
 
   // ---- per-segment state ---------------------------------------------------
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     auto load_k = [&](int i) __attribute__((always_inline)) {
       const int ks = i / C::KT, kt = i % C::KT;
       const int r = kt * 16 + m16;
-      return as_bf16x8(*reinterpret_cast<const u32x4*>(tk + r * C::RB + (((ks * 4 + g4) ^ swz<D>(r)) << 4)));
+      return as_bf16x8(*reinterpret_cast<const u32x4*>(tk + r * C::RB + (((ks * 4 + g4) ^ swz_k<D>(r)) << 4)));
     };
 #pragma unroll
     for (int kt = 0; kt < C::KT; ++kt)
@@ -358,8 +361,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
       const int s2 = i / C::DT, dt = i % C::DT;
       const int d = dt * 16 + vc;
       const int r0 = s2 * 32 + vr, r1 = r0 + 16;
-      const unsigned char* p0 = tv + r0 * C::RB + (((d >> 3) ^ swz<D>(r0)) << 4) + ((d & 7) << 1);
-      const unsigned char* p1 = tv + r1 * C::RB + (((d >> 3) ^ swz<D>(r1)) << 4) + ((d & 7) << 1);
+      const unsigned char* p0 = tv + r0 * C::RB + (((d >> 3) ^ swz_v<D>(r0)) << 4) + ((d & 7) << 1);
+      const unsigned char* p1 = tv + r1 * C::RB + (((d >> 3) ^ swz_v<D>(r1)) << 4) + ((d & 7) << 1);
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p0);
       const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)p1);
       const u32x4 w = {__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
@@ -399,9 +402,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   // ---- prologue: K_0, V_0, K_1 -------------------------------------------
   if (my_n > 0) {
     begin_segment(qb_of(0));
-    issue_tile(sK0[grp], Kh, kb_of(0));
-    issue_tile(sV0[grp], Vh, kb_of(0));
-    if (my_n > 1) issue_tile(sK1[grp], Kh, kb_of(1));
+    issue_tile(sK0[grp], Kh, koff, kb_of(0));
+    issue_tile(sV0[grp], Vh, voff, kb_of(0));
+    if (my_n > 1) issue_tile(sK1[grp], Kh, koff, kb_of(1));
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   __syncthreads();
@@ -430,8 +433,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     if (j >= nsteps) return;
     // V(j)
     const bool nv = j + 1 < my_n, nk = j + 2 < my_n;
-    if (nv) issue_tile(vprev, Vh, kb_of(j + 1));
-    if (nk) issue_tile(kcur, Kh, kb_of(j + 2));
+    if (nv) issue_tile(vprev, Vh, voff, kb_of(j + 1));
+    if (nk) issue_tile(kcur, Kh, koff, kb_of(j + 2));
     p_valid = s_valid;
     if (s_valid) {
       if (s_kb * BN + BN - 1 > start_pos + seg_qb * C::BM + wave * RPW) softmax(true);
