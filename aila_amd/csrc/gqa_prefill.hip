@@ -32,7 +32,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLazyRescaleLog2 = 8.0f;
-constexpr int kPrefetch = 4;   // LDS operand reads in flight ahead of their MFMAs
+constexpr int kPrefetch = 8;   // LDS operand reads in flight ahead of their MFMAs
 constexpr int kNumXcd = 8;   // MI355X: 8 accelerator complex dies, one L2 each
 // Buffer resource word 3 for raw (untyped, unswizzled) gfx9 buffer loads.
 constexpr int kBufferRsrcWord3 = 0x00020000;
