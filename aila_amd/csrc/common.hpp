@@ -133,6 +133,66 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+
+// ---- LDS DMA and scheduling helpers ---------------------------------------
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+
+// Buffer resource word 3 for raw (untyped, unswizzled) gfx9 buffer loads.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// Workgroup barrier that orders LDS accesses only (no wait for outstanding
+// global loads or LDS DMAs).
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Raw buffer resource (gfx9 layout): 48-bit base, stride 0, num_records in
+// bytes, word 3 = untyped raw access. Loads past num_records return zeros.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, int num_bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu,
+               static_cast<uint32_t>(num_bytes), static_cast<uint32_t>(kBufferRsrcWord3)};
+}
+
+// One wave-wide 16-byte-per-lane buffer load written straight to LDS: lane l
+// lands at lds + 16*l (the wave's KiB is contiguous). Issued as inline asm so
+// the compiler does not treat the LDS tiles as pending DMA targets (it would
+// wait for every DMA in flight before any LDS read); kernels order these
+// writes themselves with counted vmcnt waits and barriers. M0 is a reserved
+// register: it is saved and restored around the load.
+__device__ __forceinline__ void dma16_to_lds_at(const u32x4& rsrc, int voffset, uint32_t m0) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+               "buffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(voffset), "s"(rsrc), "s"(m0)
+               : "memory");
+}
+__device__ __forceinline__ void dma16_to_lds(const u32x4& rsrc, int voffset, void* lds) {
+  dma16_to_lds_at(rsrc, voffset, static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+}
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most N vector
+// memory operations of this wave are outstanding; expcnt and lgkmcnt are
+// left at their maxima (not waited on).
+template <int N>
+constexpr int vmcnt_imm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  return (N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+// Transposing LDS read: within each 16-lane group, lane i addresses 4 bf16
+// (8 bytes) of row (base + i/4) at column (c0 + 4*(i%4)); lane j receives
+// element j of those four rows, i.e. M[base + r][c0 + j] for r = 0..3.
+__device__ __forceinline__ u32x2 ds_read_tr4(const void* lds_addr) {
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)lds_addr);
+  return __builtin_bit_cast(u32x2, v);
+}
+
 }  // namespace aila
 
 // ---- host-side error plumbing (defined in capi.hip) ---------------------

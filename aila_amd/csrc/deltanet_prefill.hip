@@ -17,17 +17,27 @@
 //             P[t,s] = e^(G_t-G_s) iq_t ik_s (Q K^T)[t,s]          (s <= t)
 //   S1      = e^(G_last) S0 + K^T (fk D),      fk = e^(G_last-G) ik
 // All decays are formed as exp of differences with s <= t (never a ratio),
-// so they stay in [0, 1]. The diagonal of T is applied in fp32, and the
-// state update K^T (fk D) uses a hi/lo bf16 split of (fk D); every other
-// MFMA operand is either an exact bf16 input or a single bf16 rounding.
+// so they stay in [0, 1]. T is computed in fp32 (diagonal 16x16 blocks by
+// substitution, off-diagonal blocks on the fp32 matrix cores), the diagonal
+// of T is applied in fp32, and the state update K^T (fk D) uses a hi/lo bf16
+// split of (fk D); every other MFMA operand is either an exact bf16 input or
+// a single bf16 rounding.
 //
 // Kernel 1 (deltanet_chunk_prep_kernel): one workgroup per (chunk, value
-//   head, sequence), fully parallel. Writes W, U, P, K^T and the row
-//   factors to the workspace.
+//   head, sequence), fully parallel, two per CU. K, Q, V tiles arrive by
+//   DMA; it writes W, K^T, P, U and the row factors to the workspace, each
+//   in the register order of the scan's MFMA operands (16-byte loads there).
 // Kernel 2 (deltanet_chunk_scan_kernel): one workgroup per (16-column slab
 //   of dv, value head, sequence); walks the chunks in order with its
 //   [dk x 16] state slab in registers (C layout of v_mfma_f32_16x16x32),
-//   exchanging MFMA operands between its 4 waves through LDS.
+//   prefetching the operands of chunk c+2 into registers while chunk c
+//   computes, and exchanging D and S between its 4 waves through LDS.
+//
+// Token/key "slot" order: every MFMA that contracts over an index whose
+// B operand is published from C-layout registers (the state rows, the
+// tokens of D) uses, within each 32-wide k-step, the order in which lane
+// group g (= lane / 16) supplies k = {4g..4g+3, 16+4g..16+4g+3}. The
+// workspace stores W (over k), K^T and P (over tokens) in that order.
 #include "common.hpp"
 
 namespace aila {
@@ -35,6 +45,7 @@ namespace {
 
 constexpr int kC = 64;          // chunk length
 constexpr int kThreads = 256;
+constexpr int kNumXcd = 8;      // MI355X: 8 accelerator complex dies, one L2 each
 
 __device__ __forceinline__ float softplus_f(float x) {
   if (x > 20.0f) return x;
@@ -42,77 +53,83 @@ __device__ __forceinline__ float softplus_f(float x) {
   return log1pf(expf(x));
 }
 
-// Workspace record of one (sequence, value head, chunk).
-template <int DK, int DV>
-struct ChunkRec {
-  static constexpr size_t kW = 0;                                   // bf16 [C][DK]
-  static constexpr size_t kU = kW + size_t(kC) * DK * 2;            // f32  [C][DV]
-  static constexpr size_t kP = kU + size_t(kC) * DV * 4;            // bf16 [C][C]
-  static constexpr size_t kKt = kP + size_t(kC) * kC * 2;           // bf16 [DK][C]
-  static constexpr size_t kF = kKt + size_t(DK) * kC * 2;           // f32 fq[C], fk[C], gam
-  static constexpr size_t kBytes = ((kF + (2 * kC + 16) * 4) + 255) / 256 * 256;
-};
+// Position of index x (within its 32-wide k-step) in slot order, and back.
+__device__ __forceinline__ int slot_pos(int x) {
+  const int i = x & 31;
+  const int p = (i < 16) ? 8 * (i >> 2) + (i & 3) : 8 * ((i - 16) >> 2) + 4 + (i & 3);
+  return (x & ~31) | p;
+}
+__device__ __forceinline__ int slot_idx(int g, int e) { return (e < 4) ? 4 * g + e : 16 + 4 * g + (e - 4); }
 
-__device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
-
-__device__ __forceinline__ bf16x8_t cat8(const u32x2& a, const u32x2& b) {
-  u32x4 r = {a[0], a[1], b[0], b[1]};
+__device__ __forceinline__ bf16x8_t cat8x2(const u32x2& a, const u32x2& b) {
+  const u32x4 r = {a[0], a[1], b[0], b[1]};
   return as_bf16x8(r);
 }
 
+// 16-byte chunk swizzles of 256-byte LDS rows (see gqa_prefill: bit 0 from
+// row bit 0 suits ds_read_b128 row reads; bit 0 from row bit 3 suits the
+// transposed reads).
+__device__ __forceinline__ int swz_rows(int r) { return r & 15; }
+__device__ __forceinline__ int swz_tr(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+
+// Workspace record of one (sequence, value head, chunk).
+template <int DK, int DV>
+struct ChunkRec {
+  static constexpr size_t kF = 0;                                   // f32 fq[C], fk[C], gamma
+  static constexpr size_t kW = 1024;                                // bf16 [C][DK], k in slot order
+  static constexpr size_t kKt = kW + size_t(kC) * DK * 2;           // bf16 [DK][C], t in slot order
+  static constexpr size_t kP = kKt + size_t(DK) * kC * 2;           // bf16 [C][C], s in slot order
+  static constexpr size_t kU = kP + size_t(kC) * kC * 2;            // f32 [DV/16][4][64 lanes][4]
+  static constexpr size_t kBytes = (kU + size_t(kC) * DV * 4 + 255) / 256 * 256;
+};
+
 // ---------------------------------------------------------------------------
 template <int DK, int DV>
-__global__ __launch_bounds__(kThreads) void deltanet_chunk_prep_kernel(
+__global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ a, const bf16* __restrict__ bg, const bf16* __restrict__ dt_bias,
     const float* __restrict__ A_log, unsigned char* __restrict__ ws, int T, int Hk, int Hv,
     float eps) {
   using R = ChunkRec<DK, DV>;
-  constexpr int KP = DK + 8;       // row pitch of K/Q tiles (bf16)
-  constexpr int TP = kC + 8;       // row pitch of transposed tiles (bf16)
-  constexpr int AP = kC + 1;       // fp32 pitch of A / To
-  __shared__ __attribute__((aligned(16))) bf16 sK[kC * KP];
-  __shared__ __attribute__((aligned(16))) bf16 sQ[kC * KP];
-  __shared__ __attribute__((aligned(16))) bf16 sKt[DK * TP];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[DV * TP];
-  __shared__ float sA[kC * AP];
-  __shared__ float sT[kC * AP];
-  __shared__ float sR[3 * 256];
-  __shared__ float sG[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
+  static_assert(DK == 128 && DV == 128, "tiles of 64 rows x 256 bytes");
+  constexpr int RB = DK * 2;       // bytes per K/Q/V row
+  constexpr int NC = DK / 8;       // 16-byte chunks per row
+  __shared__ __attribute__((aligned(1024))) unsigned char sK[kC * RB];    // K, swz_rows
+  __shared__ __attribute__((aligned(1024))) unsigned char sQA[kC * RB];   // Q (swz_rows), then A fp32 [64][64]
+  __shared__ __attribute__((aligned(1024))) unsigned char sVW[kC * RB];   // V (swz_tr), then W staging
+  __shared__ __attribute__((aligned(16))) float sT[kC * kC];              // To, fp32 [64][64]
+  __shared__ __attribute__((aligned(16))) bf16 sP[kC * kC];               // P staging (slot order)
+  __shared__ __attribute__((aligned(16))) float sScr[4][256];             // per-wave 16x16 scratch
+  __shared__ float sG2[kC], sGn[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
+  float* sA = reinterpret_cast<float*>(sQA);
 
   const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
   const int nch = (T + kC - 1) / kC;
   const int hk = hv / (Hv / Hk);
   const int t0 = c * kC;
   const int n = min(kC, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m16 = lane & 15, g4 = lane >> 4;
   unsigned char* rec = ws + ((static_cast<size_t>(b) * Hv + hv) * nch + c) * R::kBytes;
 
-  // ---- 1. stage K, Q (row-major), K^T, V^T ---------------------------------
-  for (int idx = tid; idx < kC * (DK / 8); idx += kThreads) {
-    const int r = idx / (DK / 8), c8 = idx % (DK / 8);
-    u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u};
-    if (r < n) {
-      const size_t row = (static_cast<size_t>(b) * T + t0 + r) * Hk + hk;
-      kv = ld16(k + row * DK + c8 * 8);
-      qv = ld16(q + row * DK + c8 * 8);
+  // ---- 1. K, Q, V tiles by DMA (rows past T read as zeros) --------------------
+  {
+    const int kq_row = Hk * DK * 2, v_row = Hv * DV * 2;   // source row strides (bytes)
+    const u32x4 rk = buffer_rsrc(k + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
+    const u32x4 rq = buffer_rsrc(q + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
+    const u32x4 rv = buffer_rsrc(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV, (n - 1) * v_row + RB);
+#pragma unroll
+    for (int i = 0; i < kC * NC / kThreads; ++i) {
+      const int slot = i * 4 + wave;                       // wave-contiguous KiB
+      const int p = slot * 64 + lane;
+      const int r = p / NC, cc = p % NC;
+      dma16_to_lds(rk, r * kq_row + ((cc ^ swz_rows(r)) << 4), sK + slot * 1024);
+      dma16_to_lds(rq, r * kq_row + ((cc ^ swz_rows(r)) << 4), sQA + slot * 1024);
+      dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
     }
-    *reinterpret_cast<u32x4*>(&sK[r * KP + c8 * 8]) = kv;
-    *reinterpret_cast<u32x4*>(&sQ[r * KP + c8 * 8]) = qv;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      sKt[(c8 * 8 + e) * TP + r] = static_cast<bf16>((e & 1) ? (kv[e >> 1] >> 16) : (kv[e >> 1] & 0xffffu));
   }
-  for (int idx = tid; idx < kC * (DV / 8); idx += kThreads) {
-    const int r = idx / (DV / 8), c8 = idx % (DV / 8);
-    u32x4 vv = {0u, 0u, 0u, 0u};
-    if (r < n) vv = ld16(v + ((static_cast<size_t>(b) * T + t0 + r) * Hv + hv) * DV + c8 * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      sVt[(c8 * 8 + e) * TP + r] = static_cast<bf16>((e & 1) ? (vv[e >> 1] >> 16) : (vv[e >> 1] & 0xffffu));
-  }
-  // gates of this chunk (wave 0): beta, g, inclusive prefix sum G
+  // gates of this chunk (wave 0, overlapping the DMA): beta, g, prefix sum G
   if (wave == 0) {
     float beta = 0.f, g = 0.f;
     if (lane < n) {
@@ -128,18 +145,30 @@ __global__ __launch_bounds__(kThreads) void deltanet_chunk_prep_kernel(
       const float o = __shfl_up(G, off);
       if (lane >= off) G += o;
     }
-    sG[lane] = G;
+    sGn[lane] = G;
+    sG2[lane] = G * kLog2e;
     sBeta[lane] = beta;
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   __syncthreads();
-  // row norms: 4 threads per row, for K and Q
+
+  auto row_chunk = [&](const unsigned char* tile, int r, int cs) __attribute__((always_inline)) {
+    return *reinterpret_cast<const u32x4*>(tile + r * RB + ((cs ^ swz_rows(r)) << 4));
+  };
+  // ---- 2. row norms: 4 threads per row ------------------------------------------
   {
     const int r = tid >> 2, part = tid & 3;
     float sk = 0.f, sq = 0.f;
-    for (int d = part * (DK / 4); d < (part + 1) * (DK / 4); ++d) {
-      const float kf = bf2f(sK[r * KP + d]), qf = bf2f(sQ[r * KP + d]);
-      sk += kf * kf;
-      sq += qf * qf;
+#pragma unroll
+    for (int cc = 0; cc < NC / 4; ++cc) {
+      float kf[8], qf[8];
+      unpack8(row_chunk(sK, r, part * (NC / 4) + cc), kf);
+      unpack8(row_chunk(sQA, r, part * (NC / 4) + cc), qf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sk = fmaf(kf[e], kf[e], sk);
+        sq = fmaf(qf[e], qf[e], sq);
+      }
     }
     sk += __shfl_xor(sk, 1);
     sk += __shfl_xor(sk, 2);
@@ -149,180 +178,255 @@ __global__ __launch_bounds__(kThreads) void deltanet_chunk_prep_kernel(
       const float ik = 1.0f / sqrtf(sk + eps);
       sIk[r] = ik;
       sIq[r] = 1.0f / sqrtf(sq + eps);
-      sSw[r] = sBeta[r] * expf(sG[r]) * ik;
+      sSw[r] = sBeta[r] * expf(sGn[r]) * ik;
     }
   }
   __syncthreads();
 
-  // ---- 2. K K^T and Q K^T (lower tiles) on MFMA -------------------------------
-  // tile list: (ti, tj) with tj <= ti: 10 tiles per product, 20 in total.
-  bf16* Pout = reinterpret_cast<bf16*>(rec + R::kP);
-  for (int job = wave; job < 20; job += 4) {
+  // ---- 3. K K^T and Q K^T lower tiles on MFMA ---------------------------------
+  // 10 tiles (ti >= tj) per product; wave w takes jobs w, w+4, ... of 20.
+  f32x4 acc3[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int job = wave + 4 * i;
     const bool isq = job >= 10;
-    int tl = isq ? job - 10 : job;
-    int ti = 0;
+    int tl = isq ? job - 10 : job, ti = 0;
     while (tl > ti) { tl -= ti + 1; ++ti; }
     const int tj = tl;
-    const bf16* X = isq ? sQ : sK;
+    const unsigned char* X = isq ? sQA : sK;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks) {
-      const bf16x8_t av = as_bf16x8(*reinterpret_cast<const u32x4*>(&X[(ti * 16 + m16) * KP + ks * 32 + g4 * 8]));
-      const bf16x8_t bv = as_bf16x8(*reinterpret_cast<const u32x4*>(&sK[(tj * 16 + m16) * KP + ks * 32 + g4 * 8]));
-      acc = mfma16x16x32(av, bv, acc);
-    }
+    for (int ks = 0; ks < DK / 32; ++ks)
+      acc = mfma16x16x32(as_bf16x8(row_chunk(X, ti * 16 + m16, ks * 4 + g4)),
+                         as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4)), acc);
+    acc3[i] = acc;
+  }
+  __syncthreads();   // Q is no longer read: its space becomes A
+  // upper tiles of P are zero
+  for (int idx = tid; idx < kC * kC; idx += kThreads) {
+    const int t = idx / kC, s = idx % kC;
+    if ((s >> 4) > (t >> 4)) sP[t * kC + slot_pos(s)] = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int job = wave + 4 * i;
+    const bool isq = job >= 10;
+    int tl = isq ? job - 10 : job, ti = 0;
+    while (tl > ti) { tl -= ti + 1; ++ti; }
+    const int tj = tl;
     const int s = tj * 16 + m16;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = ti * 16 + g4 * 4 + j;
+      const float dec = fast_exp2(sG2[t] - sG2[s]);   // s <= t where used: <= 1
       if (!isq) {
-        const float val = (s < t) ? sBeta[t] * expf(sG[t] - sG[s]) * sIk[t] * sIk[s] * acc[j] : 0.f;
-        sA[t * AP + s] = val;
-        if (ti != tj) sA[s * AP + t] = 0.f;     // upper triangle
+        sA[t * kC + s] = (s < t) ? sBeta[t] * sIk[t] * sIk[s] * dec * acc3[i][j] : 0.f;
       } else {
-        const float val = (s <= t) ? expf(sG[t] - sG[s]) * sIq[t] * sIk[s] * acc[j] : 0.f;
-        Pout[t * kC + s] = f2bf(val);
-        if (ti != tj) Pout[s * kC + t] = 0;
+        sP[t * kC + slot_pos(s)] = f2bf((s <= t) ? sIq[t] * sIk[s] * dec * acc3[i][j] : 0.f);
       }
     }
   }
   __syncthreads();
 
-  // ---- 3. To = (I + A)^-1 - I, blocked by 16 ----------------------------------
-  // 3a. diagonal blocks: wave w, lane j < 16 owns column j of block w.
-  if (m16 == lane) {   // lanes 0..15 of each wave
-    const int base = wave * 16;
-    const int j = lane;
-    float tc[16];
+  // ---- 4. To = (I + A)^-1 - I ---------------------------------------------------
+  // 4a. diagonal block w by substitution: lane (g4, m16) owns column m16 and
+  //     the partial sums over rows m = 4*g4 .. 4*g4+3 of the block.
+  {
+    const int base = wave * 16, j = m16;
+    float xl[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) tc[i] = 0.f;
+    for (int kk = 0; kk < 4; ++kk) xl[kk] = (4 * g4 + kk == j) ? 1.f : 0.f;
 #pragma unroll
     for (int i = 1; i < 16; ++i) {
-      if (j < i) {
-        float acc = sA[(base + i) * AP + base + j];
+      const f32x4 arow = *reinterpret_cast<const f32x4*>(&sA[(base + i) * kC + base + 4 * g4]);
+      float part = arow[0] * xl[0];
 #pragma unroll
-        for (int m = 1; m < 16; ++m)
-          if (m > j && m < i) acc += sA[(base + i) * AP + base + m] * tc[m];
-        tc[i] = -acc;
-      }
+      for (int kk = 1; kk < 4; ++kk) part = fmaf(arow[kk], xl[kk], part);   // A[i][m] = 0 for m >= i
+      const float sum = xrow4_sum(part);
+      const float xi = (i > j) ? -sum : ((i == j) ? 1.f : 0.f);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        if (4 * g4 + kk == i) xl[kk] = xi;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sT[(base + i) * AP + base + j] = tc[i];
+    for (int kk = 0; kk < 4; ++kk) {
+      const int i = 4 * g4 + kk;
+      sT[(base + i) * kC + base + j] = (i > j) ? xl[kk] : 0.f;
+    }
   }
-  // clear the strictly-upper blocks of sT
+  // strictly-upper blocks of To are zero
   for (int idx = tid; idx < kC * kC; idx += kThreads) {
     const int r = idx / kC, cc = idx % kC;
-    if ((cc >> 4) > (r >> 4)) sT[r * AP + cc] = 0.f;
+    if ((cc >> 4) > (r >> 4)) sT[idx] = 0.f;
   }
   __syncthreads();
-  // 3b. off-diagonal blocks by distance d: T_IJ = -(I + To_II) R,
-  //     R = sum_{M=J}^{I-1} A_IM T_MJ with T_JJ = I + To_JJ.
+  // 4b. off-diagonal blocks by distance d on the fp32 matrix cores:
+  //     T_IJ = -(I + To_II) R,  R = sum_{M=J}^{I-1} A_IM T_MJ,  T_JJ = I + To_JJ.
+  auto prod = [&](f32x4 acc, const float* X, int xr, int xc, const float* Y, int yr, int yc, int ypitch)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[(xr + m16) * kC + xc + 4 * kk + g4],
+                                                 Y[(yr + 4 * kk + g4) * ypitch + yc + m16], acc, 0, 0, 0);
+    return acc;
+  };
   for (int d = 1; d < 4; ++d) {
-    const int nblk = 4 - d;
-    for (int e = tid; e < nblk * 256; e += kThreads) {
-      const int J = e >> 8, I = J + d;
-      const int i = (e >> 4) & 15, j = e & 15;
-      const int row = I * 16 + i, col = J * 16 + j;
-      float acc = sA[row * AP + col];           // M = J, identity part of T_JJ
-      for (int m = J * 16; m < I * 16; ++m) acc += sA[row * AP + m] * sT[m * AP + col];
-      sR[e] = acc;
-    }
-    __syncthreads();
-    for (int e = tid; e < nblk * 256; e += kThreads) {
-      const int J = e >> 8, I = J + d;
-      const int i = (e >> 4) & 15, j = e & 15;
-      float acc = sR[e];
-      for (int m = 0; m < i; ++m) acc += sT[(I * 16 + i) * AP + I * 16 + m] * sR[(J << 8) + (m << 4) + j];
-      sT[(I * 16 + i) * AP + J * 16 + j] = -acc;
+    if (wave < 4 - d) {
+      const int J = wave, I = J + d;
+      f32x4 r;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) r[jj] = sA[(I * 16 + 4 * g4 + jj) * kC + J * 16 + m16];
+      r = prod(r, sA, I * 16, J * 16, sT, J * 16, J * 16, kC);             // A_IJ To_JJ
+      for (int M = J + 1; M < I; ++M) r = prod(r, sA, I * 16, M * 16, sT, M * 16, J * 16, kC);
+      float* scr = sScr[wave];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) scr[(4 * g4 + jj) * 16 + m16] = r[jj];
+      f32x4 tr = prod(r, sT, I * 16, I * 16, scr, 0, 0, 16);               // R + To_II R
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) sT[(I * 16 + 4 * g4 + jj) * kC + J * 16 + m16] = -tr[jj];
     }
     __syncthreads();
   }
 
-  // ---- 4. W and U: wave w owns token tile w ---------------------------------
+  // ---- 5. U = bf16(To diag(beta)) V + diag(beta) V, then W likewise with K ----
+  // wave w owns token tile w; A operands in slot order over s, B operands by
+  // transposing reads of the V / K tiles in the same order.
+  const int ti = wave;
+  const int nks = ti / 2 + 1;                     // k-steps of 32 tokens up to the diagonal
+  auto a_operand = [&](int ks, const float* fac) __attribute__((always_inline)) {
+    const int t = ti * 16 + m16;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int s = ks * 32 + slot_idx(g4, e);
+      f[e] = sT[t * kC + s] * fac[s];
+    }
+    const u32x4 w = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
+    return as_bf16x8(w);
+  };
+  auto b_operand = [&](const unsigned char* tile, bool trswz, int ks, int dt) __attribute__((always_inline)) {
+    const int d = dt * 16 + 4 * (m16 & 3);
+    const int r0 = ks * 32 + 4 * g4 + (m16 >> 2), r1 = r0 + 16;
+    const int z0 = trswz ? swz_tr(r0) : swz_rows(r0), z1 = trswz ? swz_tr(r1) : swz_rows(r1);
+    const u32x2 lo = ds_read_tr4(tile + r0 * RB + (((d >> 3) ^ z0) << 4) + ((d & 7) << 1));
+    const u32x2 hi = ds_read_tr4(tile + r1 * RB + (((d >> 3) ^ z1) << 4) + ((d & 7) << 1));
+    const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
+    return as_bf16x8(w);
+  };
+  auto tile_elem = [&](const unsigned char* tile, bool trswz, int r, int d) __attribute__((always_inline)) {
+    const int z = trswz ? swz_tr(r) : swz_rows(r);
+    return bf2f(*reinterpret_cast<const bf16*>(tile + r * RB + (((d >> 3) ^ z) << 4) + ((d & 7) << 1)));
+  };
   {
-    const int ti = wave;
-    const int nks = ti / 2 + 1;     // k-steps of 32 tokens below the diagonal
-    bf16x8_t aw[2], au[2];
+    bf16x8_t au[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (ks < nks) {
-        const int t = ti * 16 + m16;
-        float wv[8], uv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int s = ks * 32 + g4 * 8 + e;
-          const float tv = sT[t * AP + s];
-          wv[e] = tv * sSw[s];
-          uv[e] = tv * sBeta[s];
-        }
-        u32x4 pw = {pack_bf16x2(wv[0], wv[1]), pack_bf16x2(wv[2], wv[3]), pack_bf16x2(wv[4], wv[5]), pack_bf16x2(wv[6], wv[7])};
-        u32x4 pu = {pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3]), pack_bf16x2(uv[4], uv[5]), pack_bf16x2(uv[6], uv[7])};
-        aw[ks] = as_bf16x8(pw);
-        au[ks] = as_bf16x8(pu);
-      }
-    }
-    bf16* Wout = reinterpret_cast<bf16*>(rec + R::kW);
+    for (int ks = 0; ks < 2; ++ks)
+      if (ks < nks) au[ks] = a_operand(ks, sBeta);
     float* Uout = reinterpret_cast<float*>(rec + R::kU);
-#pragma unroll
-    for (int dt = 0; dt < DK / 16; ++dt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks < nks) {
-          const bf16x8_t bv = as_bf16x8(*reinterpret_cast<const u32x4*>(&sKt[(dt * 16 + m16) * TP + ks * 32 + g4 * 8]));
-          acc = mfma16x16x32(aw[ks], bv, acc);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = ti * 16 + g4 * 4 + j, dd = dt * 16 + m16;
-        const float w = acc[j] + sSw[t] * bf2f(sK[t * KP + dd]);
-        Wout[t * DK + dd] = f2bf(w);
-      }
-    }
 #pragma unroll
     for (int dt = 0; dt < DV / 16; ++dt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks < nks) {
-          const bf16x8_t bv = as_bf16x8(*reinterpret_cast<const u32x4*>(&sVt[(dt * 16 + m16) * TP + ks * 32 + g4 * 8]));
-          acc = mfma16x16x32(au[ks], bv, acc);
-        }
+      for (int ks = 0; ks < 2; ++ks)
+        if (ks < nks) acc = mfma16x16x32(au[ks], b_operand(sVW, true, ks, dt), acc);
+      f32x4 u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = ti * 16 + g4 * 4 + j;
+        u[j] = acc[j] + sBeta[t] * tile_elem(sVW, true, t, dt * 16 + m16);
       }
+      *reinterpret_cast<f32x4*>(&Uout[((dt * 4 + ti) * 64 + lane) * 4]) = u;   // C-layout order
+    }
+  }
+  __syncthreads();   // V is no longer read: its space stages W
+  {
+    bf16x8_t aw[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      if (ks < nks) aw[ks] = a_operand(ks, sSw);
+    bf16* Ws = reinterpret_cast<bf16*>(sVW);       // [C][DK], k in slot order
+#pragma unroll
+    for (int dt = 0; dt < DK / 16; ++dt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        if (ks < nks) acc = mfma16x16x32(aw[ks], b_operand(sK, false, ks, dt), acc);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = ti * 16 + g4 * 4 + j, dd = dt * 16 + m16;
-        Uout[t * DV + dd] = acc[j] + sBeta[t] * bf2f(sVt[dd * TP + t]);
+        Ws[t * DK + slot_pos(dd)] = f2bf(acc[j] + sSw[t] * tile_elem(sK, false, t, dd));
       }
     }
   }
-  // ---- 5. K^T and the row factors ---------------------------------------------
-  bf16* Ktout = reinterpret_cast<bf16*>(rec + R::kKt);
-  for (int idx = tid; idx < DK * (kC / 8); idx += kThreads) {
-    const int r = idx / (kC / 8), c8 = idx % (kC / 8);
-    *reinterpret_cast<u32x4*>(&Ktout[r * kC + c8 * 8]) = *reinterpret_cast<const u32x4*>(&sKt[r * TP + c8 * 8]);
+  // ---- 6. K^T in slot order over tokens, straight from transposing reads --------
+  {
+    bf16* Ktout = reinterpret_cast<bf16*>(rec + R::kKt);
+    // 2 token k-steps x DK/16 key tiles = 16 jobs, 4 per wave
+#pragma unroll
+    for (int i = 0; i < 2 * (DK / 16) / 4; ++i) {
+      const int job = wave * (2 * (DK / 16) / 4) + i;
+      const int ks = job & 1, dt = job >> 1;
+      const bf16x8_t op = b_operand(sK, false, ks, dt);   // K[tokens in slot order][dt*16 + m16]
+      *reinterpret_cast<u32x4*>(&Ktout[(dt * 16 + m16) * kC + ks * 32 + g4 * 8]) = __builtin_bit_cast(u32x4, op);
+    }
+  }
+  __syncthreads();
+  // ---- 7. W and P out (16-byte stores), row factors ------------------------------
+  {
+    const u32x4* Ws = reinterpret_cast<const u32x4*>(sVW);
+    u32x4* Wout = reinterpret_cast<u32x4*>(rec + R::kW);
+#pragma unroll
+    for (int i = 0; i < kC * DK * 2 / 16 / kThreads; ++i) Wout[i * kThreads + tid] = Ws[i * kThreads + tid];
+    const u32x4* Ps = reinterpret_cast<const u32x4*>(sP);
+    u32x4* Pout = reinterpret_cast<u32x4*>(rec + R::kP);
+#pragma unroll
+    for (int i = 0; i < kC * kC * 2 / 16 / kThreads; ++i) Pout[i * kThreads + tid] = Ps[i * kThreads + tid];
   }
   float* F = reinterpret_cast<float*>(rec + R::kF);
   if (tid < kC) {
-    const float Glast = sG[n - 1];
-    F[tid] = (tid < n) ? expf(sG[tid]) * sIq[tid] : 0.f;            // fq
-    F[kC + tid] = (tid < n) ? expf(Glast - sG[tid]) * sIk[tid] : 0.f;  // fk
+    const float Glast = sGn[n - 1];
+    F[tid] = (tid < n) ? expf(sGn[tid]) * sIq[tid] : 0.f;            // fq
+    F[kC + tid] = (tid < n) ? expf(Glast - sGn[tid]) * sIk[tid] : 0.f;  // fk
     if (tid == 0) F[2 * kC] = expf(Glast);                          // gamma
   }
 }
 
 // ---------------------------------------------------------------------------
+// Operands of one chunk, in registers (loaded two chunks ahead).
+struct ScanOps {
+  u32x4 w[4];        // W rows, k-steps 0..3 (slot order)
+  u32x2 qa[4], qb[4];// Q rows, k-steps 0..3, slots 0..3 and 4..7
+  u32x4 p[2];        // P rows, token k-steps 0..1
+  u32x4 kt[2][2];    // K^T rows [tile][token k-step]
+  f32x4 u;           // U (C layout)
+  f32x4 fq, fk;      // row factors of the 4 output rows
+  float gam;
+};
+
 template <int DK, int DV>
-__global__ __launch_bounds__(kThreads) void deltanet_chunk_scan_kernel(
+__global__ __launch_bounds__(kThreads, 1) void deltanet_chunk_scan_kernel(
     const bf16* __restrict__ q, const unsigned char* __restrict__ ws, float* __restrict__ state,
     bf16* __restrict__ out, int T, int Hk, int Hv, float scale) {
   using R = ChunkRec<DK, DV>;
   static_assert(DK == 4 * 32, "the four waves own 32 key rows each");
-  const int slab = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+  // XCD-aware placement: workgroups are dispatched round-robin over the 8
+  // XCDs, so linear id i runs on XCD i % 8. All DV/16 slabs of one head are
+  // put on the same XCD, where they share the head's chunk records in L2
+  // (otherwise every XCD fetches them from HBM).
+  constexpr int kSlabs = DV / 16;
+  const int nhead = static_cast<int>(gridDim.y * gridDim.z);
+  const int lin = blockIdx.x + kSlabs * (blockIdx.y + static_cast<int>(gridDim.y) * blockIdx.z);
+  int slab = blockIdx.x, headlin = blockIdx.y + static_cast<int>(gridDim.y) * blockIdx.z;
+  if (kSlabs == kNumXcd && nhead % kNumXcd == 0) {
+    const int xcd = lin % kNumXcd, i = lin / kNumXcd;
+    slab = i % kSlabs;
+    headlin = xcd + kNumXcd * (i / kSlabs);
+  }
+  const int hv = headlin % Hv, b = headlin / Hv;
   const int nch = (T + kC - 1) / kC;
   const int hk = hv / (Hv / Hk);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m16 = lane & 15, g4 = lane >> 4;
   const int col = slab * 16 + m16;
 
@@ -331,6 +435,47 @@ __global__ __launch_bounds__(kThreads) void deltanet_chunk_scan_kernel(
   __shared__ u32x2 sDh[2][2][64];        // (fk D) hi
   __shared__ u32x2 sDl[2][2][64];        // (fk D) lo
 
+  const unsigned char* recs = ws + (static_cast<size_t>(b) * Hv + hv) * nch * R::kBytes;
+  // Operand loads of one chunk, in three parts that the chunk before last
+  // issues at three points of its own work (issued at once, 21 loads per
+  // wave stall the wave while the memory pipe drains the other waves').
+  auto load_part = [&](int part, int c, ScanOps& o) __attribute__((always_inline)) {
+    const unsigned char* rec = recs + static_cast<size_t>(c) * R::kBytes;
+    const int trow = wave * 16 + m16;
+    if (part == 0) {
+      const bf16* W = reinterpret_cast<const bf16*>(rec + R::kW) + trow * DK + g4 * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) o.w[ks] = ld16(W + ks * 32);
+      const int tq = min(c * kC + trow, T - 1);
+      const bf16* qrow = q + ((static_cast<size_t>(b) * T + tq) * Hk + hk) * DK + g4 * 4;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        o.qa[ks] = *reinterpret_cast<const u32x2*>(qrow + ks * 32);
+        o.qb[ks] = *reinterpret_cast<const u32x2*>(qrow + ks * 32 + 16);
+      }
+    } else if (part == 1) {
+      const bf16* P = reinterpret_cast<const bf16*>(rec + R::kP) + trow * kC + g4 * 8;
+      o.p[0] = ld16(P);
+      o.p[1] = ld16(P + 32);
+      o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + wave) * 64 + lane) * 16);
+      const float* F = reinterpret_cast<const float*>(rec + R::kF);
+      o.fq = *reinterpret_cast<const f32x4*>(F + wave * 16 + g4 * 4);
+      o.fk = *reinterpret_cast<const f32x4*>(F + kC + wave * 16 + g4 * 4);
+      o.gam = F[2 * kC];
+    } else {
+      const bf16* Kt = reinterpret_cast<const bf16*>(rec + R::kKt) + g4 * 8;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = ld16(Kt + (wave * 32 + tt * 16 + m16) * kC + s2 * 32);
+    }
+  };
+  auto load_ops = [&](int c, ScanOps& o) __attribute__((always_inline)) {
+    load_part(0, c, o);
+    load_part(1, c, o);
+    load_part(2, c, o);
+  };
+
   // state slab in C layout: rows 32*wave + 16*tt + 4*g4 + j, column col
   float* Sg = state + (static_cast<size_t>(b) * Hv + hv) * DK * DV;
   float s_reg[2][4];
@@ -338,97 +483,102 @@ __global__ __launch_bounds__(kThreads) void deltanet_chunk_scan_kernel(
   for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s_reg[tt][j] = Sg[static_cast<size_t>(wave * 32 + tt * 16 + g4 * 4 + j) * DV + col];
-
-  auto publish_state = [&]() {
+  auto publish_state = [&]() __attribute__((always_inline)) {
     u32x4 w = {pack_bf16x2(s_reg[0][0], s_reg[0][1]), pack_bf16x2(s_reg[0][2], s_reg[0][3]),
                pack_bf16x2(s_reg[1][0], s_reg[1][1]), pack_bf16x2(s_reg[1][2], s_reg[1][3])};
     sS[wave][lane] = w;
   };
-  publish_state();
-  __syncthreads();
 
-  for (int c = 0; c < nch; ++c) {
+  // Chunk c with operands o; loads the operands of chunk cn into on.
+  auto chunk = [&](int c, const ScanOps& o, int cn, ScanOps& on) __attribute__((always_inline)) {
     const int t0 = c * kC;
     const int n = min(kC, T - t0);
-    const unsigned char* rec = ws + ((static_cast<size_t>(b) * Hv + hv) * nch + c) * R::kBytes;
-    const bf16* W = reinterpret_cast<const bf16*>(rec + R::kW);
-    const float* U = reinterpret_cast<const float*>(rec + R::kU);
-    const bf16* P = reinterpret_cast<const bf16*>(rec + R::kP);
-    const bf16* Kt = reinterpret_cast<const bf16*>(rec + R::kKt);
-    const float* F = reinterpret_cast<const float*>(rec + R::kF);
-
-    // ---- D = U - W S and Q S for token tile `wave` ----------------------------
-    const int trow = wave * 16 + m16;                 // A-operand row (token)
-    const int tq = min(t0 + trow, T - 1);
-    const bf16* qrow = q + ((static_cast<size_t>(b) * T + tq) * Hk + hk) * DK;
+    load_part(0, cn, on);
+    // D = U - W S and Q S for token tile `wave`
     f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f}, qs_acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < DK / 32; ++ks) {
-      const int k0 = ks * 32 + g4 * 4;
-      const bf16x8_t aW = cat8(ld8(W + trow * DK + k0), ld8(W + trow * DK + k0 + 16));
-      const bf16x8_t aQ = cat8(ld8(qrow + k0), ld8(qrow + k0 + 16));
       const bf16x8_t bS = as_bf16x8(sS[ks][lane]);
-      ws_acc = mfma16x16x32(aW, bS, ws_acc);
-      qs_acc = mfma16x16x32(aQ, bS, qs_acc);
+      ws_acc = mfma16x16x32(as_bf16x8(o.w[ks]), bS, ws_acc);
+      const u32x4 qv = {o.qa[ks][0], o.qa[ks][1], o.qb[ks][0], o.qb[ks][1]};
+      qs_acc = mfma16x16x32(as_bf16x8(qv), bS, qs_acc);
     }
     float dval[4], dsc[4];
     f32x4 o_acc;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = wave * 16 + g4 * 4 + j;
-      dval[j] = U[t * DV + col] - ws_acc[j];
-      dsc[j] = F[kC + t] * dval[j];
-      o_acc[j] = F[t] * qs_acc[j];
+      dval[j] = o.u[j] - ws_acc[j];
+      dsc[j] = o.fk[j] * dval[j];
+      o_acc[j] = o.fq[j] * qs_acc[j];
     }
     // publish D (bf16) and fk*D (hi/lo) as B operands of the 32-token k-steps
     {
       const int s2 = wave >> 1, half = wave & 1;
       sD[s2][half][lane] = u32x2{pack_bf16x2(dval[0], dval[1]), pack_bf16x2(dval[2], dval[3])};
       float hi[4], lo[4];
+      const u32x2 hp = {pack_bf16x2(dsc[0], dsc[1]), pack_bf16x2(dsc[2], dsc[3])};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        hi[j] = bf2f(f2bf(dsc[j]));
+        hi[j] = __uint_as_float((j & 1) ? (hp[j >> 1] & 0xffff0000u) : (hp[j >> 1] << 16));
         lo[j] = dsc[j] - hi[j];
       }
-      sDh[s2][half][lane] = u32x2{pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3])};
+      sDh[s2][half][lane] = hp;
       sDl[s2][half][lane] = u32x2{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3])};
     }
     __syncthreads();
-
-    // ---- O += P D ; store ---------------------------------------------------------
+    load_part(1, cn, on);
+    // O += P D ; store
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      if (s2 <= (wave >> 1)) {
-        const int k0 = s2 * 32 + g4 * 4;
-        const bf16x8_t aP = cat8(ld8(P + trow * kC + k0), ld8(P + trow * kC + k0 + 16));
-        const u32x2 lo2 = sD[s2][0][lane], hi2 = sD[s2][1][lane];
-        o_acc = mfma16x16x32(aP, cat8(lo2, hi2), o_acc);
+      if (s2 <= (wave >> 1))
+        o_acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), o_acc);
+    }
+    {
+      bf16* orow = out + ((static_cast<size_t>(b) * T + t0 + wave * 16 + g4 * 4) * Hv + hv) * DV + col;
+      const size_t rs = static_cast<size_t>(Hv) * DV;
+      if (n == kC) {   // full chunk: no per-row guard
+#pragma unroll
+        for (int j = 0; j < 4; ++j) orow[j * rs] = f2bf(scale * o_acc[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (wave * 16 + g4 * 4 + j < n) orow[j * rs] = f2bf(scale * o_acc[j]);
       }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = wave * 16 + g4 * 4 + j;
-      if (t < n) out[((static_cast<size_t>(b) * T + t0 + t) * Hv + hv) * DV + col] = f2bf(scale * o_acc[j]);
-    }
-
-    // ---- S = gamma S + K^T (fk D) for key rows of this wave ------------------------
-    const float gam = F[2 * kC];
+    load_part(2, cn, on);
+    // S = gamma S + K^T (fk D) for the key rows of this wave
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int krow = wave * 32 + tt * 16 + m16;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const int k0 = s2 * 32 + g4 * 4;
-        const bf16x8_t aK = cat8(ld8(Kt + krow * kC + k0), ld8(Kt + krow * kC + k0 + 16));
-        acc = mfma16x16x32(aK, cat8(sDh[s2][0][lane], sDh[s2][1][lane]), acc);
-        acc = mfma16x16x32(aK, cat8(sDl[s2][0][lane], sDl[s2][1][lane]), acc);
+        const bf16x8_t aK = as_bf16x8(o.kt[tt][s2]);
+        acc = mfma16x16x32(aK, cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), acc);
+        acc = mfma16x16x32(aK, cat8x2(sDl[s2][0][lane], sDl[s2][1][lane]), acc);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s_reg[tt][j] = gam * s_reg[tt][j] + acc[j];
+      for (int j = 0; j < 4; ++j) s_reg[tt][j] = o.gam * s_reg[tt][j] + acc[j];
     }
     publish_state();
     __syncthreads();
+  };
+
+  publish_state();
+  // Three operand sets rotate: the loads of chunk c+2 are in flight while
+  // chunk c computes (the compiler's vmcnt waits cover them exactly).
+  // The loads are unconditional (clamped to the last chunk) so that the
+  // compiler's wait counts stay exact: a conditional load would make every
+  // later wait fall back to vmcnt(0), draining the prefetch.
+  ScanOps o0, o1, o2;
+  load_ops(0, o0);
+  load_ops(min(1, nch - 1), o1);
+  __syncthreads();
+  for (int c = 0; c < nch; c += 3) {
+    chunk(c, o0, min(c + 2, nch - 1), o2);
+    if (c + 1 >= nch) break;
+    chunk(c + 1, o1, min(c + 3, nch - 1), o0);
+    if (c + 2 >= nch) break;
+    chunk(c + 2, o2, min(c + 4, nch - 1), o1);
   }
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt)

@@ -34,8 +34,6 @@ constexpr int kThreads = 64 * kWaves;
 constexpr float kLazyRescaleLog2 = 8.0f;
 constexpr int kPrefetch = 8;   // LDS operand reads in flight ahead of their MFMAs
 constexpr int kNumXcd = 8;   // MI355X: 8 accelerator complex dies, one L2 each
-// Buffer resource word 3 for raw (untyped, unswizzled) gfx9 buffer loads.
-constexpr int kBufferRsrcWord3 = 0x00020000;
 
 template <int D, int RPW, int BN>
 struct PrefillCfg {
@@ -74,51 +72,6 @@ template <int D>
 __device__ __forceinline__ int swz_v(int r) {
   if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);
   else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
-}
-
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-
-// Workgroup barrier that orders LDS accesses only (no wait for outstanding
-// global loads or LDS DMAs).
-__device__ __forceinline__ void phase_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Raw buffer resource (gfx9 layout): 48-bit base, stride 0, num_records in
-// bytes, word 3 = untyped raw access. Loads past num_records return zeros.
-__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, int num_bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu,
-               static_cast<uint32_t>(num_bytes), static_cast<uint32_t>(kBufferRsrcWord3)};
-}
-
-// One wave-wide 16-byte-per-lane buffer load written straight to LDS: lane l
-// lands at lds + 16*l (the wave's KiB is contiguous). Issued as inline asm so
-// the compiler does not treat the LDS tiles as pending DMA targets (it would
-// wait for every DMA in flight before any LDS read); the kernel orders these
-// writes itself with counted vmcnt waits and barriers.
-__device__ __forceinline__ void dma16_to_lds_at(const u32x4& rsrc, int voffset, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voffset), "s"(rsrc), "s"(m0)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_to_lds(const u32x4& rsrc, int voffset, void* lds) {
-  dma16_to_lds_at(rsrc, voffset, static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-}
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
-
-// s_waitcnt immediate (gfx9 encoding) that waits until at most N vector
-// memory operations of this wave are outstanding; expcnt and lgkmcnt are
-// left at their maxima (not waited on).
-template <int N>
-constexpr int vmcnt_imm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  return (N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
 // One workgroup = two 4-wave groups and one head. It owns a balanced pair of
