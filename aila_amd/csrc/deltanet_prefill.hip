@@ -27,11 +27,12 @@
 //   head, sequence), fully parallel, two per CU. K, Q, V tiles arrive by
 //   DMA; it writes W, K^T, P, U and the row factors to the workspace, each
 //   in the register order of the scan's MFMA operands (16-byte loads there).
-// Kernel 2 (deltanet_chunk_scan_kernel): one workgroup per (16-column slab
-//   of dv, value head, sequence); walks the chunks in order with its
-//   [dk x 16] state slab in registers (C layout of v_mfma_f32_16x16x32),
-//   prefetching the operands of chunk c+2 into registers while chunk c
-//   computes, and exchanging D and S between its 4 waves through LDS.
+// Kernel 2 (deltanet_chunk_scan_kernel): one 8-wave workgroup per (16-column
+//   slab of dv, value head, sequence); walks the chunks in order with its
+//   [dk x 16] state slab in registers (C layout of v_mfma_f32_16x16x32) of
+//   four "state" waves while four "output" waves form the outputs beside
+//   them; each wave prefetches its own operands of chunk c+2 into registers
+//   while chunk c computes, and D and S are exchanged through LDS.
 //
 // Token/key "slot" order: every MFMA that contracts over an index whose
 // B operand is published from C-layout registers (the state rows, the
@@ -72,14 +73,24 @@ __device__ __forceinline__ bf16x8_t cat8x2(const u32x2& a, const u32x2& b) {
 __device__ __forceinline__ int swz_rows(int r) { return r & 15; }
 __device__ __forceinline__ int swz_tr(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-// Workspace record of one (sequence, value head, chunk).
+// Workspace record of one (sequence, value head, chunk). Every scan operand
+// is stored in register order - [tile][k-step][lane][16 bytes] - so that one
+// wave load is one contiguous KiB (a 16-row gather would cost the memory
+// pipe 16 cache lines per instruction).
+//   W  [4 token tiles][4 k-steps][64][8 bf16]    W[16w+l%16][32ks + slots of l/16]
+//   Kt [8 key tiles][2 token k-steps][64][8 bf16] K[32s2 + slots of l/16][16dt+l%16]
+//   P  [4 token tiles][2 k-steps][64][8 bf16]    P[16w+l%16][32s2 + slots of l/16]
+//   Q  [4 token tiles][4 k-steps][64][8 bf16]    Q[16w+l%16][32ks + slots of l/16]
+//   U  [DV/16 slabs][4 token tiles][64][4 f32]   C layout of U
+//   F  fq[C], fk[C], gamma (f32)
 template <int DK, int DV>
 struct ChunkRec {
-  static constexpr size_t kF = 0;                                   // f32 fq[C], fk[C], gamma
-  static constexpr size_t kW = 1024;                                // bf16 [C][DK], k in slot order
-  static constexpr size_t kKt = kW + size_t(kC) * DK * 2;           // bf16 [DK][C], t in slot order
-  static constexpr size_t kP = kKt + size_t(DK) * kC * 2;           // bf16 [C][C], s in slot order
-  static constexpr size_t kU = kP + size_t(kC) * kC * 2;            // f32 [DV/16][4][64 lanes][4]
+  static constexpr size_t kF = 0;
+  static constexpr size_t kW = 1024;
+  static constexpr size_t kKt = kW + size_t(kC) * DK * 2;
+  static constexpr size_t kP = kKt + size_t(DK) * kC * 2;
+  static constexpr size_t kQ = kP + size_t(kC) * kC * 2;
+  static constexpr size_t kU = kQ + size_t(kC) * DK * 2;
   static constexpr size_t kBytes = (kU + size_t(kC) * DV * 4 + 255) / 256 * 256;
 };
 
@@ -182,6 +193,21 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
   }
   __syncthreads();
+
+  // ---- 2b. Q in register order for the scan (before its tile becomes A) ------
+  {
+    u32x4* Qout = reinterpret_cast<u32x4*>(rec + R::kQ);
+#pragma unroll
+    for (int i = 0; i < kC * DK * 2 / 16 / kThreads; ++i) {
+      const int o = i * kThreads + tid;             // [tile][k-step][lane]
+      const int l = o & 63, ks = (o >> 6) & 3, tw = o >> 8;
+      const int r = tw * 16 + (l & 15), g = l >> 4;
+      const int k0 = ks * 32 + 4 * g, k1 = k0 + 16;   // slots 0..3 and 4..7
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(sQA + r * RB + (((k0 >> 3) ^ swz_rows(r)) << 4) + ((k0 & 7) << 1));
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(sQA + r * RB + (((k1 >> 3) ^ swz_rows(r)) << 4) + ((k1 & 7) << 1));
+      Qout[o] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  }
 
   // ---- 3. K K^T and Q K^T lower tiles on MFMA ---------------------------------
   // 10 tiles (ti >= tj) per product; wave w takes jobs w, w+4, ... of 20.
@@ -367,20 +393,28 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int job = wave * (2 * (DK / 16) / 4) + i;
       const int ks = job & 1, dt = job >> 1;
       const bf16x8_t op = b_operand(sK, false, ks, dt);   // K[tokens in slot order][dt*16 + m16]
-      *reinterpret_cast<u32x4*>(&Ktout[(dt * 16 + m16) * kC + ks * 32 + g4 * 8]) = __builtin_bit_cast(u32x4, op);
+      *reinterpret_cast<u32x4*>(&Ktout[((dt * 2 + ks) * 64 + lane) * 8]) = __builtin_bit_cast(u32x4, op);
     }
   }
   __syncthreads();
   // ---- 7. W and P out (16-byte stores), row factors ------------------------------
   {
-    const u32x4* Ws = reinterpret_cast<const u32x4*>(sVW);
+    // staged [t][slot position] -> register order [tile][k-step][lane]
+    const bf16* Ws = reinterpret_cast<const bf16*>(sVW);
     u32x4* Wout = reinterpret_cast<u32x4*>(rec + R::kW);
 #pragma unroll
-    for (int i = 0; i < kC * DK * 2 / 16 / kThreads; ++i) Wout[i * kThreads + tid] = Ws[i * kThreads + tid];
-    const u32x4* Ps = reinterpret_cast<const u32x4*>(sP);
+    for (int i = 0; i < kC * DK * 2 / 16 / kThreads; ++i) {
+      const int o = i * kThreads + tid;
+      const int l = o & 63, ks = (o >> 6) & 3, tw = o >> 8;
+      Wout[o] = *reinterpret_cast<const u32x4*>(&Ws[(tw * 16 + (l & 15)) * DK + ks * 32 + (l >> 4) * 8]);
+    }
     u32x4* Pout = reinterpret_cast<u32x4*>(rec + R::kP);
 #pragma unroll
-    for (int i = 0; i < kC * kC * 2 / 16 / kThreads; ++i) Pout[i * kThreads + tid] = Ps[i * kThreads + tid];
+    for (int i = 0; i < kC * kC * 2 / 16 / kThreads; ++i) {
+      const int o = i * kThreads + tid;
+      const int l = o & 63, s2 = (o >> 6) & 1, tw = o >> 7;
+      Pout[o] = *reinterpret_cast<const u32x4*>(&sP[(tw * 16 + (l & 15)) * kC + s2 * 32 + (l >> 4) * 8]);
+    }
   }
   float* F = reinterpret_cast<float*>(rec + R::kF);
   if (tid < kC) {
@@ -392,23 +426,35 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Operands of one chunk, in registers (loaded two chunks ahead).
-struct ScanOps {
-  u32x4 w[4];        // W rows, k-steps 0..3 (slot order)
-  u32x2 qa[4], qb[4];// Q rows, k-steps 0..3, slots 0..3 and 4..7
-  u32x4 p[2];        // P rows, token k-steps 0..1
-  u32x4 kt[2][2];    // K^T rows [tile][token k-step]
+// Per-chunk operands in registers (loaded two chunks ahead), by wave role.
+struct StateOps {
+  u32x4 w[4];        // W rows of token tile w4, k-steps 0..3 (slot order)
+  u32x4 kt[2][2];    // K^T rows [key tile][token k-step]
   f32x4 u;           // U (C layout)
-  f32x4 fq, fk;      // row factors of the 4 output rows
+  f32x4 fk;          // fk of the 4 rows this lane holds
   float gam;
 };
+struct OutOps {
+  u32x4 q[4];        // Q rows of token tile w4, k-steps 0..3 (slot order)
+  u32x4 p[2];        // P rows, token k-steps 0..1
+  f32x4 fq;
+};
 
+// One workgroup = 8 waves on one (16-column slab, value head, sequence).
+// Waves 0-3 ("state" waves) carry the recurrence: each holds 32 key rows
+// of the slab's state and, per chunk, computes D = U - W S for token tile
+// w4, publishes D, then S = gamma S + K^T (fk D) for its key rows and
+// publishes S. Waves 4-7 ("output" waves) compute O = fq (Q S) + P D for
+// token tile w4 and store it. With two waves per SIMD the output path runs
+// beside the state path; the chunk's two barriers order both:
+//   A: state: W S, D, publish D        | output: Q S (S of this chunk)
+//   B: state: K^T (fk D), publish S'   | output: + P D, store
 template <int DK, int DV>
-__global__ __launch_bounds__(kThreads, 1) void deltanet_chunk_scan_kernel(
+__global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     const bf16* __restrict__ q, const unsigned char* __restrict__ ws, float* __restrict__ state,
     bf16* __restrict__ out, int T, int Hk, int Hv, float scale) {
   using R = ChunkRec<DK, DV>;
-  static_assert(DK == 4 * 32, "the four waves own 32 key rows each");
+  static_assert(DK == 4 * 32, "the four state waves own 32 key rows each");
   // XCD-aware placement: workgroups are dispatched round-robin over the 8
   // XCDs, so linear id i runs on XCD i % 8. All DV/16 slabs of one head are
   // put on the same XCD, where they share the head's chunk records in L2
@@ -424,9 +470,9 @@ __global__ __launch_bounds__(kThreads, 1) void deltanet_chunk_scan_kernel(
   }
   const int hv = headlin % Hv, b = headlin / Hv;
   const int nch = (T + kC - 1) / kC;
-  const int hk = hv / (Hv / Hk);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w4 = wave & 3;
   const int m16 = lane & 15, g4 = lane >> 4;
   const int col = slab * 16 + m16;
 
@@ -436,154 +482,145 @@ __global__ __launch_bounds__(kThreads, 1) void deltanet_chunk_scan_kernel(
   __shared__ u32x2 sDl[2][2][64];        // (fk D) lo
 
   const unsigned char* recs = ws + (static_cast<size_t>(b) * Hv + hv) * nch * R::kBytes;
-  // Operand loads of one chunk, in three parts that the chunk before last
-  // issues at three points of its own work (issued at once, 21 loads per
-  // wave stall the wave while the memory pipe drains the other waves').
-  auto load_part = [&](int part, int c, ScanOps& o) __attribute__((always_inline)) {
-    const unsigned char* rec = recs + static_cast<size_t>(c) * R::kBytes;
-    const int trow = wave * 16 + m16;
-    if (part == 0) {
-      const bf16* W = reinterpret_cast<const bf16*>(rec + R::kW) + trow * DK + g4 * 8;
+  auto rec_of = [&](int c) __attribute__((always_inline)) { return recs + static_cast<size_t>(c) * R::kBytes; };
+
+  if (wave < 4) {
+    // ------------------------------------------------------------ state waves
+    auto load = [&](int c, StateOps& o) __attribute__((always_inline)) {
+      const unsigned char* rec = rec_of(c);
+      const u32x4* W = reinterpret_cast<const u32x4*>(rec + R::kW) + w4 * 4 * 64 + lane;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) o.w[ks] = ld16(W + ks * 32);
-      const int tq = min(c * kC + trow, T - 1);
-      const bf16* qrow = q + ((static_cast<size_t>(b) * T + tq) * Hk + hk) * DK + g4 * 4;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        o.qa[ks] = *reinterpret_cast<const u32x2*>(qrow + ks * 32);
-        o.qb[ks] = *reinterpret_cast<const u32x2*>(qrow + ks * 32 + 16);
-      }
-    } else if (part == 1) {
-      const bf16* P = reinterpret_cast<const bf16*>(rec + R::kP) + trow * kC + g4 * 8;
-      o.p[0] = ld16(P);
-      o.p[1] = ld16(P + 32);
-      o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + wave) * 64 + lane) * 16);
-      const float* F = reinterpret_cast<const float*>(rec + R::kF);
-      o.fq = *reinterpret_cast<const f32x4*>(F + wave * 16 + g4 * 4);
-      o.fk = *reinterpret_cast<const f32x4*>(F + kC + wave * 16 + g4 * 4);
-      o.gam = F[2 * kC];
-    } else {
-      const bf16* Kt = reinterpret_cast<const bf16*>(rec + R::kKt) + g4 * 8;
+      for (int ks = 0; ks < 4; ++ks) o.w[ks] = W[ks * 64];
+      const u32x4* Kt = reinterpret_cast<const u32x4*>(rec + R::kKt) + lane;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = ld16(Kt + (wave * 32 + tt * 16 + m16) * kC + s2 * 32);
-    }
-  };
-  auto load_ops = [&](int c, ScanOps& o) __attribute__((always_inline)) {
-    load_part(0, c, o);
-    load_part(1, c, o);
-    load_part(2, c, o);
-  };
-
-  // state slab in C layout: rows 32*wave + 16*tt + 4*g4 + j, column col
-  float* Sg = state + (static_cast<size_t>(b) * Hv + hv) * DK * DV;
-  float s_reg[2][4];
+        for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = Kt[((w4 * 2 + tt) * 2 + s2) * 64];
+      o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + w4) * 64 + lane) * 16);
+      const float* F = reinterpret_cast<const float*>(rec + R::kF);
+      o.fk = *reinterpret_cast<const f32x4*>(F + kC + w4 * 16 + g4 * 4);
+      o.gam = F[2 * kC];
+    };
+    // state slab in C layout: rows 32*w4 + 16*tt + 4*g4 + j, column col
+    float* Sg = state + (static_cast<size_t>(b) * Hv + hv) * DK * DV;
+    float s_reg[2][4];
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s_reg[tt][j] = Sg[static_cast<size_t>(wave * 32 + tt * 16 + g4 * 4 + j) * DV + col];
-  auto publish_state = [&]() __attribute__((always_inline)) {
-    u32x4 w = {pack_bf16x2(s_reg[0][0], s_reg[0][1]), pack_bf16x2(s_reg[0][2], s_reg[0][3]),
-               pack_bf16x2(s_reg[1][0], s_reg[1][1]), pack_bf16x2(s_reg[1][2], s_reg[1][3])};
-    sS[wave][lane] = w;
-  };
-
-  // Chunk c with operands o; loads the operands of chunk cn into on.
-  auto chunk = [&](int c, const ScanOps& o, int cn, ScanOps& on) __attribute__((always_inline)) {
-    const int t0 = c * kC;
-    const int n = min(kC, T - t0);
-    load_part(0, cn, on);
-    // D = U - W S and Q S for token tile `wave`
-    f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f}, qs_acc = {0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 4; ++j) s_reg[tt][j] = Sg[static_cast<size_t>(w4 * 32 + tt * 16 + g4 * 4 + j) * DV + col];
+    auto publish_state = [&]() __attribute__((always_inline)) {
+      const u32x4 w = {pack_bf16x2(s_reg[0][0], s_reg[0][1]), pack_bf16x2(s_reg[0][2], s_reg[0][3]),
+                       pack_bf16x2(s_reg[1][0], s_reg[1][1]), pack_bf16x2(s_reg[1][2], s_reg[1][3])};
+      sS[w4][lane] = w;
+    };
+    auto chunk = [&](const StateOps& o, int cn, StateOps& on) __attribute__((always_inline)) {
+      // A: D = U - W S, published as bf16 and as hi/lo bf16 of fk D
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks) {
-      const bf16x8_t bS = as_bf16x8(sS[ks][lane]);
-      ws_acc = mfma16x16x32(as_bf16x8(o.w[ks]), bS, ws_acc);
-      const u32x4 qv = {o.qa[ks][0], o.qa[ks][1], o.qb[ks][0], o.qb[ks][1]};
-      qs_acc = mfma16x16x32(as_bf16x8(qv), bS, qs_acc);
-    }
-    float dval[4], dsc[4];
-    f32x4 o_acc;
+      for (int ks = 0; ks < DK / 32; ++ks) acc = mfma16x16x32(as_bf16x8(o.w[ks]), as_bf16x8(sS[ks][lane]), acc);
+      {
+        float dval[4], dsc[4], lo[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dval[j] = o.u[j] - ws_acc[j];
-      dsc[j] = o.fk[j] * dval[j];
-      o_acc[j] = o.fq[j] * qs_acc[j];
-    }
-    // publish D (bf16) and fk*D (hi/lo) as B operands of the 32-token k-steps
-    {
-      const int s2 = wave >> 1, half = wave & 1;
-      sD[s2][half][lane] = u32x2{pack_bf16x2(dval[0], dval[1]), pack_bf16x2(dval[2], dval[3])};
-      float hi[4], lo[4];
-      const u32x2 hp = {pack_bf16x2(dsc[0], dsc[1]), pack_bf16x2(dsc[2], dsc[3])};
+        for (int j = 0; j < 4; ++j) {
+          dval[j] = o.u[j] - acc[j];
+          dsc[j] = o.fk[j] * dval[j];
+        }
+        const int s2 = w4 >> 1, half = w4 & 1;
+        sD[s2][half][lane] = u32x2{pack_bf16x2(dval[0], dval[1]), pack_bf16x2(dval[2], dval[3])};
+        const u32x2 hp = {pack_bf16x2(dsc[0], dsc[1]), pack_bf16x2(dsc[2], dsc[3])};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        hi[j] = __uint_as_float((j & 1) ? (hp[j >> 1] & 0xffff0000u) : (hp[j >> 1] << 16));
-        lo[j] = dsc[j] - hi[j];
+        for (int j = 0; j < 4; ++j)
+          lo[j] = dsc[j] - __uint_as_float((j & 1) ? (hp[j >> 1] & 0xffff0000u) : (hp[j >> 1] << 16));
+        sDh[s2][half][lane] = hp;
+        sDl[s2][half][lane] = u32x2{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3])};
       }
-      sDh[s2][half][lane] = hp;
-      sDl[s2][half][lane] = u32x2{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3])};
-    }
-    __syncthreads();
-    load_part(1, cn, on);
-    // O += P D ; store
+      load(cn, on);
+      __syncthreads();
+      // B: S = gamma S + K^T (fk D) for the key rows of this wave
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      if (s2 <= (wave >> 1))
-        o_acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), o_acc);
+      for (int tt = 0; tt < 2; ++tt) {
+        f32x4 a2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x8_t aK = as_bf16x8(o.kt[tt][s2]);
+          a2 = mfma16x16x32(aK, cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), a2);
+          a2 = mfma16x16x32(aK, cat8x2(sDl[s2][0][lane], sDl[s2][1][lane]), a2);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s_reg[tt][j] = o.gam * s_reg[tt][j] + a2[j];
+      }
+      publish_state();
+      __syncthreads();
+    };
+    publish_state();
+    // Three operand sets rotate; loads are unconditional (clamped to the
+    // last chunk) so that the compiler's wait counts stay exact.
+    StateOps o0, o1, o2;
+    load(0, o0);
+    load(min(1, nch - 1), o1);
+    __syncthreads();
+    for (int c = 0; c < nch; c += 3) {
+      chunk(o0, min(c + 2, nch - 1), o2);
+      if (c + 1 >= nch) break;
+      chunk(o1, min(c + 3, nch - 1), o0);
+      if (c + 2 >= nch) break;
+      chunk(o2, min(c + 4, nch - 1), o1);
     }
-    {
-      bf16* orow = out + ((static_cast<size_t>(b) * T + t0 + wave * 16 + g4 * 4) * Hv + hv) * DV + col;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Sg[static_cast<size_t>(w4 * 32 + tt * 16 + g4 * 4 + j) * DV + col] = s_reg[tt][j];
+  } else {
+    // ----------------------------------------------------------- output waves
+    auto load = [&](int c, OutOps& o) __attribute__((always_inline)) {
+      const unsigned char* rec = rec_of(c);
+      const u32x4* Q = reinterpret_cast<const u32x4*>(rec + R::kQ) + w4 * 4 * 64 + lane;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) o.q[ks] = Q[ks * 64];
+      const u32x4* P = reinterpret_cast<const u32x4*>(rec + R::kP) + w4 * 2 * 64 + lane;
+      o.p[0] = P[0];
+      o.p[1] = P[64];
+      o.fq = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(rec + R::kF) + w4 * 16 + g4 * 4);
+    };
+    auto chunk = [&](int c, const OutOps& o, int cn, OutOps& on) __attribute__((always_inline)) {
+      const int t0 = c * kC;
+      const int n = min(kC, T - t0);
+      // A: Q S with the state of this chunk
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < DK / 32; ++ks) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sS[ks][lane]), acc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] *= o.fq[j];
+      load(cn, on);
+      __syncthreads();
+      // B: + P D, store
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+        if (s2 <= (w4 >> 1)) acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), acc);
+      bf16* orow = out + ((static_cast<size_t>(b) * T + t0 + w4 * 16 + g4 * 4) * Hv + hv) * DV + col;
       const size_t rs = static_cast<size_t>(Hv) * DV;
       if (n == kC) {   // full chunk: no per-row guard
 #pragma unroll
-        for (int j = 0; j < 4; ++j) orow[j * rs] = f2bf(scale * o_acc[j]);
+        for (int j = 0; j < 4; ++j) orow[j * rs] = f2bf(scale * acc[j]);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (wave * 16 + g4 * 4 + j < n) orow[j * rs] = f2bf(scale * o_acc[j]);
+          if (w4 * 16 + g4 * 4 + j < n) orow[j * rs] = f2bf(scale * acc[j]);
       }
-    }
-    load_part(2, cn, on);
-    // S = gamma S + K^T (fk D) for the key rows of this wave
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const bf16x8_t aK = as_bf16x8(o.kt[tt][s2]);
-        acc = mfma16x16x32(aK, cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), acc);
-        acc = mfma16x16x32(aK, cat8x2(sDl[s2][0][lane], sDl[s2][1][lane]), acc);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s_reg[tt][j] = o.gam * s_reg[tt][j] + acc[j];
-    }
-    publish_state();
+      __syncthreads();
+    };
+    OutOps o0, o1, o2;
+    load(0, o0);
+    load(min(1, nch - 1), o1);
     __syncthreads();
-  };
-
-  publish_state();
-  // Three operand sets rotate: the loads of chunk c+2 are in flight while
-  // chunk c computes (the compiler's vmcnt waits cover them exactly).
-  // The loads are unconditional (clamped to the last chunk) so that the
-  // compiler's wait counts stay exact: a conditional load would make every
-  // later wait fall back to vmcnt(0), draining the prefetch.
-  ScanOps o0, o1, o2;
-  load_ops(0, o0);
-  load_ops(min(1, nch - 1), o1);
-  __syncthreads();
-  for (int c = 0; c < nch; c += 3) {
-    chunk(c, o0, min(c + 2, nch - 1), o2);
-    if (c + 1 >= nch) break;
-    chunk(c + 1, o1, min(c + 3, nch - 1), o0);
-    if (c + 2 >= nch) break;
-    chunk(c + 2, o2, min(c + 4, nch - 1), o1);
+    for (int c = 0; c < nch; c += 3) {
+      chunk(c, o0, min(c + 2, nch - 1), o2);
+      if (c + 1 >= nch) break;
+      chunk(c + 1, o1, min(c + 3, nch - 1), o0);
+      if (c + 2 >= nch) break;
+      chunk(c + 2, o2, min(c + 4, nch - 1), o1);
+    }
   }
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) Sg[static_cast<size_t>(wave * 32 + tt * 16 + g4 * 4 + j) * DV + col] = s_reg[tt][j];
 }
 
 }  // namespace
@@ -616,7 +653,7 @@ extern "C" int aila_hip_deltanet_prefill(const void* q, const void* k, const voi
                      static_cast<const bf16*>(a), static_cast<const bf16*>(b),
                      static_cast<const bf16*>(dt_bias), A_log, static_cast<unsigned char*>(workspace), T,
                      Hk, Hv, eps);
-  hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128>), dim3(dv / 16, Hv, B), dim3(kThreads), 0, st,
+  hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128>), dim3(dv / 16, Hv, B), dim3(2 * kThreads), 0, st,
                      static_cast<const bf16*>(q), static_cast<const unsigned char*>(workspace), state,
                      static_cast<bf16*>(out), T, Hk, Hv, scale);
   return check_launch("deltanet_prefill");
