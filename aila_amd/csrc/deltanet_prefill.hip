@@ -54,12 +54,7 @@ __device__ __forceinline__ float softplus_f(float x) {
   return log1pf(expf(x));
 }
 
-// Position of index x (within its 32-wide k-step) in slot order, and back.
-__device__ __forceinline__ int slot_pos(int x) {
-  const int i = x & 31;
-  const int p = (i < 16) ? 8 * (i >> 2) + (i & 3) : 8 * ((i - 16) >> 2) + 4 + (i & 3);
-  return (x & ~31) | p;
-}
+// Index held by slot e (0..7) of lane group g within a 32-wide k-step.
 __device__ __forceinline__ int slot_idx(int g, int e) { return (e < 4) ? 4 * g + e : 16 + 4 * g + (e - 4); }
 
 __device__ __forceinline__ bf16x8_t cat8x2(const u32x2& a, const u32x2& b) {
@@ -107,11 +102,10 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   constexpr int NC = DK / 8;       // 16-byte chunks per row
   __shared__ __attribute__((aligned(1024))) unsigned char sK[kC * RB];    // K, swz_rows
   __shared__ __attribute__((aligned(1024))) unsigned char sQA[kC * RB];   // Q (swz_rows), then A fp32 [64][64]
-  __shared__ __attribute__((aligned(1024))) unsigned char sVW[kC * RB];   // V (swz_tr), then W staging
+  __shared__ __attribute__((aligned(1024))) unsigned char sVW[kC * RB];   // V (swz_tr)
   __shared__ __attribute__((aligned(16))) float sT[kC * kC];              // To, fp32 [64][64]
-  __shared__ __attribute__((aligned(16))) bf16 sP[kC * kC];               // P staging (slot order)
   __shared__ __attribute__((aligned(16))) float sScr[4][256];             // per-wave 16x16 scratch
-  __shared__ float sG2[kC], sGn[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
+  __shared__ __attribute__((aligned(16))) float sG2[kC], sGn[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
   float* sA = reinterpret_cast<float*>(sQA);
 
   const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
@@ -209,47 +203,72 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
   }
 
-  // ---- 3. K K^T and Q K^T lower tiles on MFMA ---------------------------------
-  // 10 tiles (ti >= tj) per product; wave w takes jobs w, w+4, ... of 20.
-  f32x4 acc3[5];
+  // ---- 3. A = masked K K^T (LDS, fp32) and P (register order, global) -------
+  // Jobs 0..9: K K^T tiles (ti >= tj). Jobs 10..17: P of token tile ti over
+  // s k-step s2, formed as P^T (operands swapped) for the two s tiles 2*s2,
+  // 2*s2+1, so that each lane holds the 8 values of its register-order slot.
+  // Wave w takes jobs w, w+4, ...; all products first (Q is read), then the
+  // epilogues.
+  f32x4 acc3[5][2];
 #pragma unroll
   for (int i = 0; i < 5; ++i) {
     const int job = wave + 4 * i;
-    const bool isq = job >= 10;
-    int tl = isq ? job - 10 : job, ti = 0;
-    while (tl > ti) { tl -= ti + 1; ++ti; }
-    const int tj = tl;
-    const unsigned char* X = isq ? sQA : sK;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    acc3[i][0] = acc3[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (job < 10) {
+      int tl = job, ti = 0;
+      while (tl > ti) { tl -= ti + 1; ++ti; }
+      const int tj = tl;
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks)
-      acc = mfma16x16x32(as_bf16x8(row_chunk(X, ti * 16 + m16, ks * 4 + g4)),
-                         as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4)), acc);
-    acc3[i] = acc;
+      for (int ks = 0; ks < DK / 32; ++ks)
+        acc3[i][0] = mfma16x16x32(as_bf16x8(row_chunk(sK, ti * 16 + m16, ks * 4 + g4)),
+                                  as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4)), acc3[i][0]);
+    } else if (job < 18) {
+      const int ti = (job - 10) >> 1, s2 = (job - 10) & 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int tj = 2 * s2 + h;
+        if (tj <= ti) {
+#pragma unroll
+          for (int ks = 0; ks < DK / 32; ++ks)
+            acc3[i][h] = mfma16x16x32(as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4)),
+                                      as_bf16x8(row_chunk(sQA, ti * 16 + m16, ks * 4 + g4)), acc3[i][h]);
+        }
+      }
+    }
   }
   __syncthreads();   // Q is no longer read: its space becomes A
-  // upper tiles of P are zero
-  for (int idx = tid; idx < kC * kC; idx += kThreads) {
-    const int t = idx / kC, s = idx % kC;
-    if ((s >> 4) > (t >> 4)) sP[t * kC + slot_pos(s)] = 0;
-  }
+  auto v4 = [&](const float* arr, int i0) __attribute__((always_inline)) { return *reinterpret_cast<const f32x4*>(arr + i0); };
+  u32x4* Pout = reinterpret_cast<u32x4*>(rec + R::kP);
 #pragma unroll
   for (int i = 0; i < 5; ++i) {
     const int job = wave + 4 * i;
-    const bool isq = job >= 10;
-    int tl = isq ? job - 10 : job, ti = 0;
-    while (tl > ti) { tl -= ti + 1; ++ti; }
-    const int tj = tl;
-    const int s = tj * 16 + m16;
+    if (job < 10) {
+      int tl = job, ti = 0;
+      while (tl > ti) { tl -= ti + 1; ++ti; }
+      const int tj = tl;
+      const int s = tj * 16 + m16, t0r = ti * 16 + g4 * 4;
+      const f32x4 bt = v4(sBeta, t0r), ikt = v4(sIk, t0r), g2t = v4(sG2, t0r);
+      const float iks = sIk[s], g2s = sG2[s];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = ti * 16 + g4 * 4 + j;
-      const float dec = fast_exp2(sG2[t] - sG2[s]);   // s <= t where used: <= 1
-      if (!isq) {
-        sA[t * kC + s] = (s < t) ? sBeta[t] * sIk[t] * sIk[s] * dec * acc3[i][j] : 0.f;
-      } else {
-        sP[t * kC + slot_pos(s)] = f2bf((s <= t) ? sIq[t] * sIk[s] * dec * acc3[i][j] : 0.f);
+      for (int j = 0; j < 4; ++j) {
+        const int t = t0r + j;
+        sA[t * kC + s] = (s < t) ? bt[j] * ikt[j] * iks * fast_exp2(g2t[j] - g2s) * acc3[i][0][j] : 0.f;
       }
+    } else if (job < 18) {
+      const int ti = (job - 10) >> 1, s2 = (job - 10) & 1;
+      const int t = ti * 16 + m16;
+      const float iqt = sIq[t], g2t = sG2[t];
+      float pv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int s0 = s2 * 32 + h * 16 + 4 * g4;
+        const f32x4 iks = v4(sIk, s0), g2s = v4(sG2, s0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          pv[4 * h + j] = (s0 + j <= t) ? iqt * iks[j] * fast_exp2(g2t - g2s[j]) * acc3[i][h][j] : 0.f;
+      }
+      Pout[(ti * 2 + s2) * 64 + lane] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
+                                              pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7])};
     }
   }
   __syncthreads();
@@ -339,10 +358,6 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
     return as_bf16x8(w);
   };
-  auto tile_elem = [&](const unsigned char* tile, bool trswz, int r, int d) __attribute__((always_inline)) {
-    const int z = trswz ? swz_tr(r) : swz_rows(r);
-    return bf2f(*reinterpret_cast<const bf16*>(tile + r * RB + (((d >> 3) ^ z) << 4) + ((d & 7) << 1)));
-  };
   {
     bf16x8_t au[2];
 #pragma unroll
@@ -355,33 +370,46 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         if (ks < nks) acc = mfma16x16x32(au[ks], b_operand(sVW, true, ks, dt), acc);
+      // diagonal term: one transposing read gives V[ti*16 + 4*g4 + j][dt*16 + m16], j = 0..3
+      const int vr = ti * 16 + 4 * g4 + (m16 >> 2), vd = dt * 16 + 4 * (m16 & 3);
+      const u32x2 vv = ds_read_tr4(sVW + vr * RB + (((vd >> 3) ^ swz_tr(vr)) << 4) + ((vd & 7) << 1));
+      const f32x4 bt = v4(sBeta, ti * 16 + g4 * 4);
       f32x4 u;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = ti * 16 + g4 * 4 + j;
-        u[j] = acc[j] + sBeta[t] * tile_elem(sVW, true, t, dt * 16 + m16);
-      }
+      for (int j = 0; j < 4; ++j)
+        u[j] = acc[j] + bt[j] * __uint_as_float((j & 1) ? (vv[j >> 1] & 0xffff0000u) : (vv[j >> 1] << 16));
       *reinterpret_cast<f32x4*>(&Uout[((dt * 4 + ti) * 64 + lane) * 4]) = u;   // C-layout order
     }
   }
-  __syncthreads();   // V is no longer read: its space stages W
+  // W^T (operands swapped: A = K^T by transposing reads, B = (To diag(sw))^T):
+  // the C layout gives lane (g4, m16) W[t = 16*tile + m16][d = 16*dt + 4*g4 + j],
+  // and d tiles 2*ks, 2*ks+1 together are its register-order slot of k-step ks.
   {
-    bf16x8_t aw[2];
+    const int t = ti * 16 + m16;
+    bf16x8_t bw[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      if (ks < nks) aw[ks] = a_operand(ks, sSw);
-    bf16* Ws = reinterpret_cast<bf16*>(sVW);       // [C][DK], k in slot order
+      if (ks < nks) bw[ks] = a_operand(ks, sSw);
+    const float swt = sSw[t];
+    u32x4* Wout = reinterpret_cast<u32x4*>(rec + R::kW);
 #pragma unroll
-    for (int dt = 0; dt < DK / 16; ++dt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kso = 0; kso < DK / 32; ++kso) {
+      float wv[8];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        if (ks < nks) acc = mfma16x16x32(aw[ks], b_operand(sK, false, ks, dt), acc);
+      for (int h = 0; h < 2; ++h) {
+        const int dt = 2 * kso + h;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = ti * 16 + g4 * 4 + j, dd = dt * 16 + m16;
-        Ws[t * DK + slot_pos(dd)] = f2bf(acc[j] + sSw[t] * tile_elem(sK, false, t, dd));
+        for (int ks = 0; ks < 2; ++ks)
+          if (ks < nks) acc = mfma16x16x32(b_operand(sK, false, ks, dt), bw[ks], acc);
+        const int d = dt * 16 + 4 * g4;
+        const u32x2 kk = *reinterpret_cast<const u32x2*>(sK + t * RB + (((d >> 3) ^ swz_rows(t)) << 4) + ((d & 7) << 1));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wv[4 * h + j] = acc[j] + swt * __uint_as_float((j & 1) ? (kk[j >> 1] & 0xffff0000u) : (kk[j >> 1] << 16));
       }
+      Wout[(ti * 4 + kso) * 64 + lane] = u32x4{pack_bf16x2(wv[0], wv[1]), pack_bf16x2(wv[2], wv[3]),
+                                               pack_bf16x2(wv[4], wv[5]), pack_bf16x2(wv[6], wv[7])};
     }
   }
   // ---- 6. K^T in slot order over tokens, straight from transposing reads --------
@@ -396,26 +424,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       *reinterpret_cast<u32x4*>(&Ktout[((dt * 2 + ks) * 64 + lane) * 8]) = __builtin_bit_cast(u32x4, op);
     }
   }
-  __syncthreads();
-  // ---- 7. W and P out (16-byte stores), row factors ------------------------------
-  {
-    // staged [t][slot position] -> register order [tile][k-step][lane]
-    const bf16* Ws = reinterpret_cast<const bf16*>(sVW);
-    u32x4* Wout = reinterpret_cast<u32x4*>(rec + R::kW);
-#pragma unroll
-    for (int i = 0; i < kC * DK * 2 / 16 / kThreads; ++i) {
-      const int o = i * kThreads + tid;
-      const int l = o & 63, ks = (o >> 6) & 3, tw = o >> 8;
-      Wout[o] = *reinterpret_cast<const u32x4*>(&Ws[(tw * 16 + (l & 15)) * DK + ks * 32 + (l >> 4) * 8]);
-    }
-    u32x4* Pout = reinterpret_cast<u32x4*>(rec + R::kP);
-#pragma unroll
-    for (int i = 0; i < kC * kC * 2 / 16 / kThreads; ++i) {
-      const int o = i * kThreads + tid;
-      const int l = o & 63, s2 = (o >> 6) & 1, tw = o >> 7;
-      Pout[o] = *reinterpret_cast<const u32x4*>(&sP[(tw * 16 + (l & 15)) * kC + s2 * 32 + (l >> 4) * 8]);
-    }
-  }
+  // ---- 7. row factors --------------------------------------------------------
   float* F = reinterpret_cast<float*>(rec + R::kF);
   if (tid < kC) {
     const float Glast = sGn[n - 1];
