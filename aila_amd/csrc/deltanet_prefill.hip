@@ -104,7 +104,6 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   __shared__ __attribute__((aligned(1024))) unsigned char sQA[kC * RB];   // Q (swz_rows), then A fp32 [64][64]
   __shared__ __attribute__((aligned(1024))) unsigned char sVW[kC * RB];   // V (swz_tr)
   __shared__ __attribute__((aligned(16))) float sT[kC * kC];              // To, fp32 [64][64]
-  __shared__ __attribute__((aligned(16))) float sScr[4][256];             // per-wave 16x16 scratch
   __shared__ __attribute__((aligned(16))) float sG2[kC], sGn[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
   float* sA = reinterpret_cast<float*>(sQA);
 
@@ -307,26 +306,30 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   __syncthreads();
   // 4b. off-diagonal blocks by distance d on the fp32 matrix cores:
   //     T_IJ = -(I + To_II) R,  R = sum_{M=J}^{I-1} A_IM T_MJ,  T_JJ = I + To_JJ.
-  auto prod = [&](f32x4 acc, const float* X, int xr, int xc, const float* Y, int yr, int yc, int ypitch)
-      __attribute__((always_inline)) {
+  // 16x16x16 products on v_mfma_f32_16x16x4f32 with the k index permuted so
+  // that at step kk lane group g supplies k = 4g + kk: the A operand of the
+  // four steps is one float4 of row m16, and a 16x16 block held in C layout
+  // (lane (g, m16) has rows 4g..4g+3 of column m16) is directly the B
+  // operand of the four steps.
+  auto prod = [&](f32x4 acc, const float* X, int xr, int xc, const f32x4& yb) __attribute__((always_inline)) {
+    const f32x4 xa = *reinterpret_cast<const f32x4*>(&X[(xr + m16) * kC + xc + 4 * g4]);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[(xr + m16) * kC + xc + 4 * kk + g4],
-                                                 Y[(yr + 4 * kk + g4) * ypitch + yc + m16], acc, 0, 0, 0);
+    for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[kk], yb[kk], acc, 0, 0, 0);
     return acc;
+  };
+  auto cblock = [&](const float* Y, int yr, int yc) __attribute__((always_inline)) {   // C layout of a block
+    f32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = Y[(yr + 4 * g4 + j) * kC + yc + m16];
+    return r;
   };
   for (int d = 1; d < 4; ++d) {
     if (wave < 4 - d) {
       const int J = wave, I = J + d;
-      f32x4 r;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) r[jj] = sA[(I * 16 + 4 * g4 + jj) * kC + J * 16 + m16];
-      r = prod(r, sA, I * 16, J * 16, sT, J * 16, J * 16, kC);             // A_IJ To_JJ
-      for (int M = J + 1; M < I; ++M) r = prod(r, sA, I * 16, M * 16, sT, M * 16, J * 16, kC);
-      float* scr = sScr[wave];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) scr[(4 * g4 + jj) * 16 + m16] = r[jj];
-      f32x4 tr = prod(r, sT, I * 16, I * 16, scr, 0, 0, 16);               // R + To_II R
+      f32x4 r = cblock(sA, I * 16, J * 16);                                 // A_IJ (identity part of T_JJ)
+      r = prod(r, sA, I * 16, J * 16, cblock(sT, J * 16, J * 16));          // + A_IJ To_JJ
+      for (int M = J + 1; M < I; ++M) r = prod(r, sA, I * 16, M * 16, cblock(sT, M * 16, J * 16));
+      const f32x4 tr = prod(r, sT, I * 16, I * 16, r);                      // R + To_II R
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) sT[(I * 16 + 4 * g4 + jj) * kC + J * 16 + m16] = -tr[jj];
     }
