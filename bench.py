@@ -77,7 +77,10 @@ def build_config5(torch, aila_amd, steps, warmup):
     dev = torch.device("cuda")
     gen = torch.Generator(device=dev)
     gen.manual_seed(0xA11A + 4)
-    max_seq = L5 + warmup + steps + 8
+    # KV capacity rounded up to a multiple of 1024 rows, as a serving engine
+    # sizes it (block-aligned): a head stride aligned to 512 KiB keeps the
+    # split-K decode's streams aligned (an odd row count costs ~7%).
+    max_seq = (L5 + warmup + steps + 8 + 1023) // 1024 * 1024
     kc, vc = [], []
     for _ in range(N_GQA):
         k = torch.empty((B5, GQA_HKV, max_seq, GQA_D), dtype=torch.bfloat16, device=dev)

@@ -56,7 +56,10 @@ size_t aila_hip_gqa_decode_workspace_size(int B, int Hq, int D);
  *               NULL for the single-pass variant (one workgroup per head
  *               group, no split; slower for long contexts).
  * Head h reads KV head h / (Hq / Hkv). Softmax scale 1/sqrt(D).
- * Supported: D in {64, 128, 256}, Hq/Hkv in {1, 2, 4, 8}. */
+ * Supported: D in {64, 128, 256}, Hq/Hkv in {1, 2, 4, 8}.
+ * Bandwidth note: a head stride max_seq*D*2 that is a multiple of 256 KiB
+ * (e.g. max_seq a multiple of 512 rows at D = 256) streams at full rate;
+ * an odd row count measured ~7% slower on MI355X. */
 int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         void* out, void* workspace, size_t workspace_bytes,
                         int B, int Hq, int Hkv, int D, int max_seq,
