@@ -35,6 +35,11 @@ _SIGS = {
     "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_deltanet_prefill_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "aila_hip_decode_prepare_qkv": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                                     _I, _I, _I, _I, _I, _I, _F, _F, _I, _P, _P], _I),
+    "aila_hip_head_rms_norm": ([_P, _P, _I, _I, _I, _F, _P], _I),
+    "aila_hip_apply_rope": ([_P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "aila_hip_sigmoid_mul": ([_P, _P, _P, ctypes.c_long, _P], _I),
     "aila_hip_deltanet_prefill": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ,
                                    _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
 }
@@ -300,4 +305,83 @@ def deltanet_prefill(q, k, v, a, b, state, out=None, workspace=None, dt_bias=Non
                                          _ptr(workspace), ws_bytes, B, T, Hk, Hv, dk, dv,
                                          float(eps), float(scale), _stream(stream))
     _check(rc, "aila_hip_deltanet_prefill")
+    return out
+
+
+# ------------------------------------------ QK-norm, RoPE, output gate ----
+def decode_prepare_qkv(q_in, k, v, q_norm_w=None, k_norm_w=None, k_cache=None, v_cache=None,
+                       pos: int = 0, positions=None, rotary_dim=None, theta: float = 1e6,
+                       eps: float = 1e-6, packed_gate: bool = False, q_out=None, gate_out=None,
+                       stream=None):
+    """Per-head RMSNorm + RoPE of one token per sequence, and the K/V append.
+
+    q_in [B,Hq,D] (or [B,Hq,2D] q|gate when ``packed_gate``); k [B,Hkv,D] is
+    updated in place; v [B,Hkv,D]; caches [B,Hkv,max_seq,D] or None. Returns
+    q_out (and gate_out when packed)."""
+    import torch
+    B, Hkv, D = k.shape
+    Hq = q_in.shape[1]
+    _need(q_in, torch.bfloat16, (B, Hq, 2 * D if packed_gate else D), "q_in")
+    _need(k, torch.bfloat16, (B, Hkv, D), "k")
+    _need(v, torch.bfloat16, (B, Hkv, D), "v")
+    if q_out is None:
+        q_out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k.device) if packed_gate else q_in
+    _need(q_out, torch.bfloat16, (B, Hq, D), "q_out")
+    if packed_gate:
+        if gate_out is None:
+            gate_out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k.device)
+        _need(gate_out, torch.bfloat16, (B, Hq, D), "gate_out")
+    for w, name in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        if w is not None:
+            _need(w, torch.bfloat16, (D,), name, align=2)
+    max_seq = 0
+    if k_cache is not None or v_cache is not None:
+        max_seq = k_cache.shape[2]
+        _need(k_cache, torch.bfloat16, (B, Hkv, max_seq, D), "k_cache")
+        _need(v_cache, torch.bfloat16, (B, Hkv, max_seq, D), "v_cache")
+    if positions is not None:
+        _need(positions, torch.int32, (B,), "positions", align=4)
+    rc = lib().aila_hip_decode_prepare_qkv(
+        _ptr(q_in), int(bool(packed_gate)), _ptr(q_out), _ptr(gate_out) if packed_gate else None,
+        _ptr(k), _ptr(v), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(k_cache), _ptr(v_cache), B, Hq, Hkv, D,
+        max_seq, D if rotary_dim is None else int(rotary_dim), float(theta), float(eps), int(pos),
+        _ptr(positions), _stream(stream))
+    _check(rc, "decode_prepare_qkv")
+    return (q_out, gate_out) if packed_gate else q_out
+
+
+def head_rms_norm(x, weight=None, eps: float = 1e-6, stream=None):
+    """In-place per-head RMSNorm of x [S, H, D] bf16 (weight [D] bf16 or None)."""
+    import torch
+    S, H, D = x.shape
+    _need(x, torch.bfloat16, (S, H, D), "x")
+    if weight is not None:
+        _need(weight, torch.bfloat16, (D,), "weight", align=2)
+    _check(lib().aila_hip_head_rms_norm(_ptr(x), _ptr(weight), S, H, D, float(eps), _stream(stream)),
+           "head_rms_norm")
+    return x
+
+
+def apply_rope(q, k, start_pos: int = 0, rotary_dim=None, theta: float = 1e6, stream=None):
+    """In-place RoPE of q [S,Hq,D] and k [S,Hkv,D] bf16 at positions start_pos + s."""
+    import torch
+    S, Hq, D = q.shape
+    Hkv = k.shape[1]
+    _need(q, torch.bfloat16, (S, Hq, D), "q")
+    _need(k, torch.bfloat16, (S, Hkv, D), "k")
+    _check(lib().aila_hip_apply_rope(_ptr(q), _ptr(k), S, int(start_pos), Hq, Hkv, D,
+                                     D if rotary_dim is None else int(rotary_dim), float(theta),
+                                     _stream(stream)), "apply_rope")
+    return q, k
+
+
+def sigmoid_mul(inp, gate, out=None, stream=None):
+    """out = inp * sigmoid(gate), bf16 tensors of equal shape (out may be inp)."""
+    import torch
+    if out is None:
+        out = torch.empty_like(inp)
+    for t, name in ((inp, "input"), (gate, "gate"), (out, "output")):
+        _need(t, torch.bfloat16, tuple(inp.shape), name)
+    _check(lib().aila_hip_sigmoid_mul(_ptr(inp), _ptr(gate), _ptr(out), inp.numel(), _stream(stream)),
+           "sigmoid_mul")
     return out

@@ -24,7 +24,7 @@ class Context {
   // Wrap an existing stream (not owned).
   explicit Context(hipStream_t s) : stream_(s), owns_stream_(false) {}
   ~Context() {
-    if (owns_stream_ && stream_) hipStreamDestroy(stream_);
+    if (owns_stream_ && stream_) (void)hipStreamDestroy(stream_);   // nothing to report from a destructor
   }
   Context(const Context&) = delete;
   Context& operator=(const Context&) = delete;
@@ -47,7 +47,7 @@ class Context {
       current_ = current_ >= it->second ? current_ - it->second : 0;
       alloc_bytes_.erase(it);
     }
-    hipFree(p);
+    (void)hipFree(p);   // free errors surface at the next synchronising call
   }
   void memcpy_h2d(void* dst, const void* src, size_t bytes) {
     hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_), "memcpy_h2d");

@@ -70,5 +70,62 @@ void linear_delta_prefill(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor&
                           Tensor& workspace, int seq_len, int num_k_heads, int num_v_heads,
                           int head_k_dim, int head_v_dim, float eps, float scale);
 
+// ---- Q/K preparation and the output gate (Ops.hpp:163-244) ----
+// Multimodal position streams (interleaved mRoPE with pos_t/pos_h/pos_w) are
+// not part of this path: the ops below throw when asked for them, and the
+// decode variants also throw on a non-zero text_pos_delta that would apply
+// (their rotary position and cache row are the same start_pos).
+
+// Per-head RMSNorm in place (Ops.hpp:165-166): x [seq_len, num_heads*head_dim]
+// bf16, weight [head_dim] bf16 (an invalid tensor means no weight).
+void head_rms_norm(Context& ctx, Tensor& x, Tensor& weight, float eps, int seq_len, int num_heads,
+                   int head_dim);
+
+// output = input * sigmoid(gate), n bf16 elements (Ops.hpp:169-170);
+// output may alias input.
+void sigmoid_mul(Context& ctx, Tensor& input, Tensor& gate, Tensor& output, int n);
+
+// NeoX RoPE in place over the full head (Ops.hpp:175-178) and over the first
+// rotary_dim dims (Ops.hpp:181-194); rotary_dim is clamped to [2, head_dim]
+// and made even. text_pos_delta shifts positions >= prompt_pos_len.
+void apply_rope(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,
+                int num_kv_heads, int head_dim, float theta);
+void apply_rope_partial(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,
+                        int num_kv_heads, int head_dim, int rotary_dim, float theta,
+                        bool interleaved = false, const int* pos_t = nullptr, const int* pos_h = nullptr,
+                        const int* pos_w = nullptr, int prompt_pos_len = 0, int text_pos_delta = 0,
+                        int mrope_section_t = 0, int mrope_section_h = 0, int mrope_section_w = 0);
+
+// One-token QK-norm + RoPE + K/V append (Ops.hpp:205-211). q [1, Hq*D] and
+// k [1, Hkv*D] are updated in place; the caches are [Hkv, max_seq, D]
+// (max_seq from k_cache.shape(1)). rope_freq is accepted and unused: the
+// backends fill it with 1/theta^(2d/head_dim) (Qwen3DenseBackend.cpp:232-236),
+// which the kernel computes itself from theta.
+void decode_prepare_qkv(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& rope_freq,
+                        Tensor& q_norm_weight, Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache,
+                        int start_pos, int num_heads_q, int num_kv_heads, int head_dim, float eps,
+                        float theta);
+
+// The same with a partial rotary width (Ops.hpp:216-230).
+void decode_prepare_qkv_partial(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& q_norm_weight,
+                                Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache, int start_pos,
+                                int num_heads_q, int num_kv_heads, int head_dim, float eps, int rotary_dim,
+                                float theta, bool interleaved = false, const int* pos_t = nullptr,
+                                const int* pos_h = nullptr, const int* pos_w = nullptr,
+                                int prompt_pos_len = 0, int text_pos_delta = 0, int mrope_section_t = 0,
+                                int mrope_section_h = 0, int mrope_section_w = 0);
+
+// Packed per-head q|gate [1, Hq*2D] split into q_out and gate_out [1, Hq*D],
+// then as decode_prepare_qkv_partial (Ops.hpp:235-250).
+void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Tensor& k, Tensor& v,
+                                        Tensor& q_out, Tensor& gate_out, Tensor& q_norm_weight,
+                                        Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache,
+                                        int start_pos, int num_heads_q, int num_kv_heads, int head_dim,
+                                        float eps, int rotary_dim, float theta, bool interleaved = false,
+                                        const int* pos_t = nullptr, const int* pos_h = nullptr,
+                                        const int* pos_w = nullptr, int prompt_pos_len = 0,
+                                        int text_pos_delta = 0, int mrope_section_t = 0,
+                                        int mrope_section_h = 0, int mrope_section_w = 0);
+
 }  // namespace ops
 }  // namespace aila

@@ -1,6 +1,7 @@
 // ops:: over the C ABI (see Ops.hpp).
 #include "Ops.hpp"
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -119,6 +120,112 @@ void linear_delta_prefill(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor&
                                   workspace.size_bytes(), 1, seq_len, num_k_heads, num_v_heads,
                                   head_k_dim, head_v_dim, eps, scale, ctx.stream()),
         "linear_delta_prefill");
+}
+
+namespace {
+
+void* opt(Tensor& t) { return t.valid() ? t.data() : nullptr; }
+
+void no_mrope(bool interleaved, const int* pos_t, const int* pos_h, const int* pos_w, const char* what) {
+  if (interleaved && pos_t && pos_h && pos_w)
+    throw std::runtime_error(std::string(what) + ": interleaved mRoPE position streams are not supported");
+}
+
+// The decode ops rotate and append at one position; a text shift that would
+// separate the two is refused.
+void no_decode_shift(int start_pos, int prompt_pos_len, int text_pos_delta, const char* what) {
+  if (text_pos_delta != 0 && start_pos >= prompt_pos_len)
+    throw std::runtime_error(std::string(what) + ": text_pos_delta is not supported");
+}
+
+}  // namespace
+
+void head_rms_norm(Context& ctx, Tensor& x, Tensor& weight, float eps, int seq_len, int num_heads,
+                   int head_dim) {
+  need_dtype(x, DType::bf16, "head_rms_norm x");
+  if (weight.valid()) need_dtype(weight, DType::bf16, "head_rms_norm weight");
+  check(aila_hip_head_rms_norm(x.data(), opt(weight), seq_len, num_heads, head_dim, eps, ctx.stream()),
+        "head_rms_norm");
+}
+
+void sigmoid_mul(Context& ctx, Tensor& input, Tensor& gate, Tensor& output, int n) {
+  need_dtype(input, DType::bf16, "sigmoid_mul input");
+  need_dtype(gate, DType::bf16, "sigmoid_mul gate");
+  need_dtype(output, DType::bf16, "sigmoid_mul output");
+  check(aila_hip_sigmoid_mul(input.data(), gate.data(), output.data(), n, ctx.stream()), "sigmoid_mul");
+}
+
+void apply_rope(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,
+                int num_kv_heads, int head_dim, float theta) {
+  apply_rope_partial(ctx, q, k, seq_len, start_pos, num_heads_q, num_kv_heads, head_dim, head_dim, theta);
+}
+
+void apply_rope_partial(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,
+                        int num_kv_heads, int head_dim, int rotary_dim, float theta, bool interleaved,
+                        const int* pos_t, const int* pos_h, const int* pos_w, int prompt_pos_len,
+                        int text_pos_delta, int, int, int) {
+  no_mrope(interleaved, pos_t, pos_h, pos_w, "apply_rope_partial");
+  need_dtype(q, DType::bf16, "apply_rope q");
+  need_dtype(k, DType::bf16, "apply_rope k");
+  // rows before prompt_pos_len rotate at their own position, the rest at
+  // position + text_pos_delta (ElementwiseOps.cpp:54-58)
+  int unshifted = text_pos_delta == 0 ? seq_len : std::max(0, std::min(seq_len, prompt_pos_len - start_pos));
+  char* qp = static_cast<char*>(q.data());
+  char* kp = static_cast<char*>(k.data());
+  if (unshifted > 0)
+    check(aila_hip_apply_rope(qp, kp, unshifted, start_pos, num_heads_q, num_kv_heads, head_dim, rotary_dim,
+                              theta, ctx.stream()),
+          "apply_rope_partial");
+  if (unshifted < seq_len) {
+    const size_t qrow = static_cast<size_t>(num_heads_q) * head_dim * 2;
+    const size_t krow = static_cast<size_t>(num_kv_heads) * head_dim * 2;
+    check(aila_hip_apply_rope(qp + unshifted * qrow, kp + unshifted * krow, seq_len - unshifted,
+                              start_pos + unshifted + text_pos_delta, num_heads_q, num_kv_heads, head_dim,
+                              rotary_dim, theta, ctx.stream()),
+          "apply_rope_partial");
+  }
+}
+
+void decode_prepare_qkv(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& rope_freq,
+                        Tensor& q_norm_weight, Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache,
+                        int start_pos, int num_heads_q, int num_kv_heads, int head_dim, float eps,
+                        float theta) {
+  (void)rope_freq;
+  decode_prepare_qkv_partial(ctx, q, k, v, q_norm_weight, k_norm_weight, k_cache, v_cache, start_pos,
+                             num_heads_q, num_kv_heads, head_dim, eps, head_dim, theta);
+}
+
+void decode_prepare_qkv_partial(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& q_norm_weight,
+                                Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache, int start_pos,
+                                int num_heads_q, int num_kv_heads, int head_dim, float eps, int rotary_dim,
+                                float theta, bool interleaved, const int* pos_t, const int* pos_h,
+                                const int* pos_w, int prompt_pos_len, int text_pos_delta, int, int, int) {
+  no_mrope(interleaved, pos_t, pos_h, pos_w, "decode_prepare_qkv_partial");
+  no_decode_shift(start_pos, prompt_pos_len, text_pos_delta, "decode_prepare_qkv_partial");
+  for (Tensor* t : {&q, &k, &v, &k_cache, &v_cache}) need_dtype(*t, DType::bf16, "decode_prepare_qkv");
+  check(aila_hip_decode_prepare_qkv(q.data(), 0, q.data(), nullptr, k.data(), v.data(), opt(q_norm_weight),
+                                    opt(k_norm_weight), k_cache.data(), v_cache.data(), 1, num_heads_q,
+                                    num_kv_heads, head_dim, static_cast<int>(k_cache.shape(1)), rotary_dim,
+                                    theta, eps, start_pos, nullptr, ctx.stream()),
+        "decode_prepare_qkv");
+}
+
+void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Tensor& k, Tensor& v,
+                                        Tensor& q_out, Tensor& gate_out, Tensor& q_norm_weight,
+                                        Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache,
+                                        int start_pos, int num_heads_q, int num_kv_heads, int head_dim,
+                                        float eps, int rotary_dim, float theta, bool interleaved,
+                                        const int* pos_t, const int* pos_h, const int* pos_w,
+                                        int prompt_pos_len, int text_pos_delta, int, int, int) {
+  no_mrope(interleaved, pos_t, pos_h, pos_w, "decode_prepare_qgkv_packed_partial");
+  no_decode_shift(start_pos, prompt_pos_len, text_pos_delta, "decode_prepare_qgkv_packed_partial");
+  for (Tensor* t : {&q_gate_packed, &k, &v, &q_out, &gate_out, &k_cache, &v_cache})
+    need_dtype(*t, DType::bf16, "decode_prepare_qgkv_packed_partial");
+  check(aila_hip_decode_prepare_qkv(q_gate_packed.data(), 1, q_out.data(), gate_out.data(), k.data(), v.data(),
+                                    opt(q_norm_weight), opt(k_norm_weight), k_cache.data(), v_cache.data(), 1,
+                                    num_heads_q, num_kv_heads, head_dim, static_cast<int>(k_cache.shape(1)),
+                                    rotary_dim, theta, eps, start_pos, nullptr, ctx.stream()),
+        "decode_prepare_qgkv_packed_partial");
 }
 
 }  // namespace ops

@@ -168,6 +168,48 @@ int aila_hip_deltanet_prefill(const void* q, const void* k, const void* v,
                               int Hv, int dk, int dv, float eps, float scale,
                               void* stream);
 
+/* ------------------------------------ QK-norm, RoPE, gate (GQA layer) --- */
+
+/* Decode-step preparation for B sequences (one token each): per-head RMSNorm
+ * of q and k (weights q_norm_w / k_norm_w [D] bf16, NULL = 1), NeoX
+ * half-split RoPE on the first rotary_dim dims (angle = position *
+ * theta^(-2d/rotary_dim)), and k/v appended to the caches at the position.
+ * Replaces ops::decode_prepare_qkv (src/ops/ElementwiseOps.cpp:105-216),
+ * ops::decode_prepare_qkv_partial (:555-705) and
+ * ops::decode_prepare_qgkv_packed_partial (:707-863, packed_gate != 0) for
+ * text positions (no mRoPE); rounding points as the reference (bf16 after
+ * the norm and after the rotation).
+ *   q_in     [B, Hq, D] bf16, or [B, Hq, 2D] (q | gate per head) if packed_gate
+ *   q_out    [B, Hq, D] bf16 (may equal q_in when not packed)
+ *   gate_out [B, Hq, D] bf16, the gate half copied through (packed_gate only)
+ *   k        [B, Hkv, D] bf16, normalised and rotated in place
+ *   v        [B, Hkv, D] bf16
+ *   k_cache/v_cache [B, Hkv, max_seq, D] bf16 or both NULL (no append)
+ *   position of sequence b: positions[b] (device int[B]) if given, else pos.
+ * Supported: D in {64, 128, 256}. */
+int aila_hip_decode_prepare_qkv(const void* q_in, int packed_gate, void* q_out, void* gate_out,
+                                void* k, const void* v, const void* q_norm_w, const void* k_norm_w,
+                                void* k_cache, void* v_cache, int B, int Hq, int Hkv, int D,
+                                int max_seq, int rotary_dim, float theta, float eps, int pos,
+                                const int* positions, void* stream);
+
+/* Per-head RMSNorm in place over x [S, H, D] bf16 with weight [D] bf16 (NULL
+ * = 1). Replaces ops::head_rms_norm (src/ops/NormOps.cpp:277-321).
+ * Supported: D in {64, 128, 256}. */
+int aila_hip_head_rms_norm(void* x, const void* weight, int S, int H, int D, float eps, void* stream);
+
+/* RoPE in place on q [S, Hq, D] and k [S, Hkv, D] bf16 at positions
+ * start_pos + s, NeoX half-split over the first rotary_dim dims. Replaces
+ * ops::apply_rope / apply_rope_partial for text positions
+ * (src/ops/ElementwiseOps.cpp:33-103). Supported: D in {64, 128, 256}. */
+int aila_hip_apply_rope(void* q, void* k, int S, int start_pos, int Hq, int Hkv, int D, int rotary_dim,
+                        float theta, void* stream);
+
+/* output = input * sigmoid(gate), n bf16 elements (output may equal input).
+ * Replaces ops::sigmoid_mul (src/ops/ElementwiseOps.cpp:519-553), the
+ * gated-attention output gate. */
+int aila_hip_sigmoid_mul(const void* input, const void* gate, void* output, long n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

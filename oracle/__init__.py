@@ -38,6 +38,9 @@ _SIGS = {
     "orc_head_rms_norm": [_P, _P, _P, _F, _I, _I, _I],
     "orc_apply_rope": [_P, _P, _I, _I, _I, _I, _I, _I, _F],
     "orc_decode_prepare_qkv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _I],
+    "orc_decode_prepare": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                           _I, _I, _I, _I, _I, _I, _F, _F, _P],
+    "orc_sigmoid_mul": [_P, _P, _P, ctypes.c_long],
     "orc_deltanet_recurrent": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _I, _I, _I, _I, _I, _I, _F, _F, _I],
     "orc_deltanet_recurrent_f64": [_P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -159,6 +162,31 @@ def decode_prepare_qkv(q, k, v, qn_w, kn_w, kc, vc, start_pos, Hq, Hkv, D, eps, 
     lib().orc_decode_prepare_qkv(_p(q), _p(k), _p(v), _p(qn_w), _p(kn_w), _p(kc), _p(vc),
                                  start_pos, Hq, Hkv, D, eps, theta, max_seq)
     return q, k
+
+
+def decode_prepare(q_in, k, v, qn_w, kn_w, kc, vc, pos, B, Hq, Hkv, D, max_seq, rotary_dim,
+                   theta, eps, packed=False):
+    """Batched decode_prepare_qkv(_partial / qgkv_packed). Returns
+    (q_out, gate_out or None, k); kc/vc (uint16 arrays or None) are updated."""
+    q_in = _c(q_in, U16)
+    k = np.array(k, dtype=U16, copy=True, order="C")
+    v, qn_w, kn_w = _c(v, U16), _c(qn_w, U16), _c(kn_w, U16)
+    q_out = np.zeros((B, Hq, D), U16)
+    gate = np.zeros((B, Hq, D), U16) if packed else None
+    posa = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (B,)))
+    if kc is not None:
+        assert kc.dtype == U16 and vc.dtype == U16 and kc.flags.c_contiguous
+    lib().orc_decode_prepare(_p(q_in), int(bool(packed)), _p(q_out), _p(gate), _p(k), _p(v), _p(qn_w),
+                             _p(kn_w), _p(kc), _p(vc), B, Hq, Hkv, D, max_seq, rotary_dim, theta, eps,
+                             _p(posa))
+    return q_out, gate, k
+
+
+def sigmoid_mul(x, g):
+    x, g = _c(x, U16), _c(g, U16)
+    o = np.zeros_like(x)
+    lib().orc_sigmoid_mul(_p(x), _p(g), _p(o), x.size)
+    return o
 
 
 def deltanet_recurrent(q, k, v, a, b, state, B, T, Hk, Hv, dk, dv, eps=1e-6,

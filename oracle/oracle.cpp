@@ -456,6 +456,48 @@ void orc_decode_prepare_qkv(bf16_t* q, bf16_t* k, const bf16_t* v,
   orc_copy_to_cache(v, vc, 1, start_pos, Hkv, D, max_seq);
 }
 
+// decode_prepare_qkv_partial (ElementwiseOps.cpp:555-705) and
+// decode_prepare_qgkv_packed_partial (:707-863), text positions, batched over
+// B independent sequences (the reference runs one): per head, q (the first
+// D of a packed [q | gate] head when packed, gate copied through) and k get
+// RMSNorm (bf16 round) then RoPE over the first `rot` dims at pos[b]
+// (bf16 round); k, v are appended to the cache row pos[b] when kc != null.
+// q_in [B,Hq,D or 2D]; q_out, gate_out [B,Hq,D]; k (in place), v [B,Hkv,D];
+// kc, vc [B,Hkv,max_seq,D].
+void orc_decode_prepare(const bf16_t* q_in, int packed, bf16_t* q_out, bf16_t* gate_out, bf16_t* k,
+                        const bf16_t* v, const bf16_t* qn_w, const bf16_t* kn_w, bf16_t* kc, bf16_t* vc,
+                        int B, int Hq, int Hkv, int D, int max_seq, int rotary_dim, float theta,
+                        float eps, const int* pos) {
+  const int qs = packed ? 2 * D : D;
+  for (int b = 0; b < B; ++b) {
+    bf16_t* qo = q_out + static_cast<size_t>(b) * Hq * D;
+    for (int h = 0; h < Hq; ++h) {
+      const bf16_t* src = q_in + (static_cast<size_t>(b) * Hq + h) * qs;
+      for (int d = 0; d < D; ++d) qo[h * D + d] = src[d];
+      if (packed)
+        for (int d = 0; d < D; ++d) gate_out[(static_cast<size_t>(b) * Hq + h) * D + d] = src[D + d];
+    }
+    bf16_t* kb = k + static_cast<size_t>(b) * Hkv * D;
+    orc_head_rms_norm(qo, qn_w, nullptr, eps, 1, Hq, D);
+    orc_head_rms_norm(kb, kn_w, nullptr, eps, 1, Hkv, D);
+    orc_apply_rope(qo, kb, 1, pos[b], Hq, Hkv, D, rotary_dim, theta);
+    if (kc) {
+      for (int h = 0; h < Hkv; ++h) {
+        const size_t row = ((static_cast<size_t>(b) * Hkv + h) * max_seq + pos[b]) * D;
+        for (int d = 0; d < D; ++d) {
+          kc[row + d] = kb[h * D + d];
+          vc[row + d] = v[(static_cast<size_t>(b) * Hkv + h) * D + d];
+        }
+      }
+    }
+  }
+}
+
+// sigmoid_mul, ElementwiseOps.cpp:519-553: o = bf16(in * 1/(1+e^-g)).
+void orc_sigmoid_mul(const bf16_t* in, const bf16_t* g, bf16_t* o, long n) {
+  for (long i = 0; i < n; ++i) o[i] = orc_f32_to_bf16(bf(in[i]) * (1.0f / (1.0f + std::exp(-bf(g[i])))));
+}
+
 // ------------------------------------------------------- DeltaNet --------
 }  // extern "C" (templates below need C++ linkage)
 // softplus, Qwen35HybridTextBackend.cpp:128-132.

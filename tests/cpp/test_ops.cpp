@@ -20,6 +20,12 @@ void orc_copy_to_cache(const uint16_t*, uint16_t*, int, int, int, int, int);
 void orc_deltanet_recurrent(const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*,
                             const uint16_t*, const uint16_t*, const float*, float*, float*, uint16_t*, int,
                             int, int, int, int, int, float, float, int);
+void orc_head_rms_norm(uint16_t*, const uint16_t*, const float*, float, int, int, int);
+void orc_apply_rope(uint16_t*, uint16_t*, int, int, int, int, int, int, float);
+void orc_decode_prepare(const uint16_t*, int, uint16_t*, uint16_t*, uint16_t*, const uint16_t*, const uint16_t*,
+                        const uint16_t*, uint16_t*, uint16_t*, int, int, int, int, int, int, float, float,
+                        const int*);
+void orc_sigmoid_mul(const uint16_t*, const uint16_t*, uint16_t*, long);
 uint16_t orc_f32_to_bf16(float);
 float orc_bf16_to_f32(uint16_t);
 }
@@ -184,6 +190,74 @@ int main() {
     double eo = relerr(download<uint16_t>(ctx, out), ob);
     expect(es <= 1e-3, "linear_delta prefill+decode state", es);
     expect(eo <= 1e-2, "linear_delta prefill+decode outputs", eo);
+  }
+  // ---- QK-norm / RoPE / decode prep / output gate -------------------------
+  {
+    const int Hq = 16, Hkv = 4, D = 256, rot = 64, max_seq = 2048, pos = 1500, S = 40;
+    const float eps = 1e-6f, theta = 1e7f;
+    u16v qg = rand_bf16(size_t(Hq) * 2 * D), k = rand_bf16(size_t(Hkv) * D), v = rand_bf16(size_t(Hkv) * D);
+    u16v qw = rand_bf16(D), kw = rand_bf16(D);
+    Tensor tqg = upload(ctx, qg, {1, Hq * 2 * D}, DType::bf16), tk = upload(ctx, k, {1, Hkv * D}, DType::bf16),
+           tv = upload(ctx, v, {1, Hkv * D}, DType::bf16), tqw = upload(ctx, qw, {D}, DType::bf16),
+           tkw = upload(ctx, kw, {D}, DType::bf16);
+    Tensor qo = Tensor::allocate(ctx, {1, Hq * D}), go = Tensor::allocate(ctx, {1, Hq * D});
+    Tensor kc = Tensor::allocate(ctx, {Hkv, max_seq, D}), vc = Tensor::allocate(ctx, {Hkv, max_seq, D});
+    ops::decode_prepare_qgkv_packed_partial(ctx, tqg, tk, tv, qo, go, tqw, tkw, kc, vc, pos, Hq, Hkv, D, eps, rot,
+                                            theta);
+    u16v wq(size_t(Hq) * D), wg(size_t(Hq) * D), wk = k;
+    const int p1 = pos;
+    orc_decode_prepare(qg.data(), 1, wq.data(), wg.data(), wk.data(), v.data(), qw.data(), kw.data(), nullptr,
+                       nullptr, 1, Hq, Hkv, D, 0, rot, theta, eps, &p1);
+    u16v gk = download<uint16_t>(ctx, tk), ck = download<uint16_t>(ctx, kc), cv = download<uint16_t>(ctx, vc);
+    bool rows = true;
+    for (int h = 0; h < Hkv; ++h)
+      rows &= !std::memcmp(&ck[(size_t(h) * max_seq + pos) * D], &gk[size_t(h) * D], D * 2) &&
+              !std::memcmp(&cv[(size_t(h) * max_seq + pos) * D], &v[size_t(h) * D], D * 2);
+    double e = std::fmax(relerr(download<uint16_t>(ctx, qo), wq), relerr(gk, wk));
+    expect(e <= 1e-2 && download<uint16_t>(ctx, go) == wg && rows, "decode_prepare_qgkv_packed_partial", e);
+    // full rotary, q in place
+    u16v q1 = rand_bf16(size_t(Hq) * D), k1 = rand_bf16(size_t(Hkv) * D);
+    Tensor tq1 = upload(ctx, q1, {1, Hq * D}, DType::bf16), tk1 = upload(ctx, k1, {1, Hkv * D}, DType::bf16);
+    Tensor freq = Tensor::allocate(ctx, {D / 2}, DType::f32);
+    ops::decode_prepare_qkv(ctx, tq1, tk1, tv, freq, tqw, tkw, kc, vc, 7, Hq, Hkv, D, eps, theta);
+    u16v wq1(size_t(Hq) * D), wk1 = k1;
+    const int p7 = 7;
+    orc_decode_prepare(q1.data(), 0, wq1.data(), nullptr, wk1.data(), v.data(), qw.data(), kw.data(), nullptr,
+                       nullptr, 1, Hq, Hkv, D, 0, D, theta, eps, &p7);
+    e = std::fmax(relerr(download<uint16_t>(ctx, tq1), wq1), relerr(download<uint16_t>(ctx, tk1), wk1));
+    expect(e <= 1e-2, "decode_prepare_qkv", e);
+    // prefill: head_rms_norm then apply_rope_partial with a text shift
+    u16v xq = rand_bf16(size_t(S) * Hq * D), xk = rand_bf16(size_t(S) * Hkv * D);
+    Tensor txq = upload(ctx, xq, {S, Hq * D}, DType::bf16), txk = upload(ctx, xk, {S, Hkv * D}, DType::bf16);
+    ops::head_rms_norm(ctx, txq, tqw, eps, S, Hq, D);
+    ops::head_rms_norm(ctx, txk, tkw, eps, S, Hkv, D);
+    const int start = 10, prompt = 25, delta = -3;
+    ops::apply_rope_partial(ctx, txq, txk, S, start, Hq, Hkv, D, rot, theta, false, nullptr, nullptr, nullptr,
+                            prompt, delta);
+    orc_head_rms_norm(xq.data(), qw.data(), nullptr, eps, S, Hq, D);
+    orc_head_rms_norm(xk.data(), kw.data(), nullptr, eps, S, Hkv, D);
+    const int n0 = prompt - start;
+    orc_apply_rope(xq.data(), xk.data(), n0, start, Hq, Hkv, D, rot, theta);
+    orc_apply_rope(xq.data() + size_t(n0) * Hq * D, xk.data() + size_t(n0) * Hkv * D, S - n0, prompt + delta, Hq,
+                   Hkv, D, rot, theta);
+    e = std::fmax(relerr(download<uint16_t>(ctx, txq), xq), relerr(download<uint16_t>(ctx, txk), xk));
+    expect(e <= 1e-2, "head_rms_norm + apply_rope_partial (text shift)", e);
+    // output gate, in place
+    const int n = 100003;
+    u16v a = rand_bf16(n), g = rand_bf16(n), wa(n);
+    Tensor ta = upload(ctx, a, {n}, DType::bf16), tg = upload(ctx, g, {n}, DType::bf16);
+    ops::sigmoid_mul(ctx, ta, tg, ta, n);
+    orc_sigmoid_mul(a.data(), g.data(), wa.data(), n);
+    e = relerr(download<uint16_t>(ctx, ta), wa);
+    expect(e <= 1e-2, "sigmoid_mul", e);
+    bool threw = false;
+    int pt[1] = {0};
+    try {
+      ops::apply_rope_partial(ctx, txq, txk, S, start, Hq, Hkv, D, rot, theta, true, pt, pt, pt, 1, 0, 8, 12, 12);
+    } catch (const std::runtime_error&) {
+      threw = true;
+    }
+    expect(threw, "apply_rope_partial rejects interleaved mRoPE", 0);
   }
   std::printf("peak device bytes %zu\n", ctx.peak_allocated_bytes());
   std::printf(g_fail ? "FAILED %d\n" : "ALL OK\n", g_fail);
