@@ -35,6 +35,8 @@ _SIGS = {
     "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_deltanet_prefill_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "aila_hip_deltanet_layer_decode": ([_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P,
+                                        _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_decode_prepare_qkv": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                                      _I, _I, _I, _I, _I, _I, _F, _F, _I, _P, _P], _I),
     "aila_hip_head_rms_norm": ([_P, _P, _I, _I, _I, _F, _P], _I),
@@ -266,6 +268,64 @@ def deltanet_decode(q, k, v, a, b, state, out=None, dt_bias=None, A_log=None,
                                         B, Hk, Hv, dk, dv, float(eps), float(scale),
                                         _stream(stream))
     _check(rc, "aila_hip_deltanet_decode")
+    return out
+
+
+def _rows(t, dtype, B, width, name, align=2):
+    """A [B, width] view whose rows may be strided (e.g. column slices of the
+    backend's fused [qkv | z | a | b] rows); returns the row stride."""
+    if t is None or not t.is_cuda or t.dtype != dtype:
+        raise ValueError(f"{name}: expected a {dtype} device tensor")
+    if t.dim() != 2 or tuple(t.shape) != (B, width) or (width > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name}: shape {tuple(t.shape)} / strides {t.stride()}, expected [{B}, {width}] "
+                         "with unit column stride")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name} must be {align}-byte aligned")
+    return t.stride(0) if B > 1 else width
+
+
+def deltanet_layer_decode(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, state, num_k_heads,
+                          out=None, conv_heads=None, dt_bias=None, A_log=None, eps: float = 1e-6,
+                          scale: float | None = None, stream=None):
+    """Full Gated DeltaNet layer step for B sequences: conv1d ring (+SiLU),
+    L2 norm, gated delta recurrence, RMSNorm(o) * norm_w * SiLU(z).
+
+    qkv [B, 2*Hk*dk + Hv*dv], z [B, Hv*dv], a/b [B, Hv] bf16 (rows may be
+    strided views); conv_w [ch, 4] bf16; conv_state [B, 3, ch] fp32 and
+    state [B, Hv, dk, dv] fp32 are updated in place; conv_head (int) or
+    conv_heads (int32 [B], device) gives the ring row of the oldest input.
+    Returns out [B, Hv*dv] bf16."""
+    import torch
+    B, Hv, dk, dv = state.shape
+    Hk = int(num_k_heads)
+    ch = 2 * Hk * dk + Hv * dv
+    qs = _rows(qkv, torch.bfloat16, B, ch, "qkv")
+    zs = _rows(z, torch.bfloat16, B, Hv * dv, "z", align=8)
+    ast = _rows(a, torch.bfloat16, B, Hv, "a")
+    bst = _rows(b, torch.bfloat16, B, Hv, "b")
+    if ast != bst:
+        raise ValueError("a and b must share one row stride")
+    K = conv_w.shape[1]
+    _need(conv_w, torch.bfloat16, (ch, K), "conv_w", align=8)
+    _need(conv_state, torch.float32, (B, K - 1, ch), "conv_state", align=4)
+    _need(norm_w, torch.float32, (dv,), "norm_w")
+    _need(state, torch.float32, (B, Hv, dk, dv), "state")
+    if conv_heads is not None:
+        _need(conv_heads, torch.int32, (B,), "conv_heads", align=4)
+    if dt_bias is not None:
+        _need(dt_bias, torch.bfloat16, (Hv,), "dt_bias", align=2)
+    if A_log is not None:
+        _need(A_log, torch.float32, (Hv,), "A_log", align=4)
+    if out is None:
+        out = torch.empty((B, Hv * dv), dtype=torch.bfloat16, device=state.device)
+    _need(out, torch.bfloat16, (B, Hv * dv), "out", align=8)
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    rc = lib().aila_hip_deltanet_layer_decode(
+        _ptr(qkv), qs, _ptr(z), zs, _ptr(a), _ptr(b), ast, _ptr(conv_w), _ptr(conv_state), int(conv_head),
+        _ptr(conv_heads), _ptr(dt_bias), _ptr(A_log), _ptr(norm_w), _ptr(state), _ptr(out), B, Hk, Hv, dk, dv,
+        K, float(eps), float(scale), _stream(stream))
+    _check(rc, "aila_hip_deltanet_layer_decode")
     return out
 
 

@@ -22,13 +22,6 @@ constexpr int kThreads = 256;
 constexpr int kColQuads = 32;   // 128 columns per workgroup
 constexpr int kRowGroups = 8;
 
-__device__ __forceinline__ float softplus_f(float x) {
-  // Qwen35HybridTextBackend.cpp:128-132
-  if (x > 20.0f) return x;
-  if (x < -20.0f) return expf(x);
-  return log1pf(expf(x));
-}
-
 template <int DK>
 __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
@@ -54,7 +47,26 @@ __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
 
   float* S = state + (static_cast<size_t>(bseq) * Hv + hv) * DK * dv;
 
-  // 1. Issue the state loads first so their latency overlaps the q/k norms.
+  // 1. The small operands (q, k, v, gates) first, then the state slab: the
+  //    norms wait only for their own loads (in-order vmcnt) while the state
+  //    loads stay in flight, and v is in registers before the update.
+  const bf16* qh = q + (static_cast<size_t>(bseq) * Hk + hk) * DK;
+  const bf16* kh = k + (static_cast<size_t>(bseq) * Hk + hk) * DK;
+  constexpr int kQK = (DK + kThreads - 1) / kThreads;
+  float qf[kQK], kf[kQK];
+#pragma unroll
+  for (int j = 0; j < kQK; ++j) {
+    const int i = t + j * kThreads < DK ? t + j * kThreads : DK - 1;
+    qf[j] = bf2f(qh[i]);
+    kf[j] = bf2f(kh[i]);
+  }
+  const size_t gi = static_cast<size_t>(bseq) * Hv + hv;
+  const float b_raw = bf2f(bgate[gi]);
+  const float a_raw = bf2f(a[gi]);
+  const float dtb = dt_bias ? bf2f(dt_bias[hv]) : 0.0f;
+  const float alog = A_log ? A_log[hv] : 0.0f;
+  const uint2 vraw = *reinterpret_cast<const uint2*>(v + gi * dv + (active ? col : 0));
+
   f32x4 s[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
@@ -64,15 +76,15 @@ __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
   }
 
   // 2. q, k L2 norms (head_l2_norm_inplace, :138-151 / :1079-1089).
-  const bf16* qh = q + (static_cast<size_t>(bseq) * Hk + hk) * DK;
-  const bf16* kh = k + (static_cast<size_t>(bseq) * Hk + hk) * DK;
   float sq = 0.f, sk = 0.f;
-  for (int i = t; i < DK; i += kThreads) {
-    const float qf = bf2f(qh[i]), kf = bf2f(kh[i]);
-    s_q[i] = qf;
-    s_k[i] = kf;
-    sq += qf * qf;
-    sk += kf * kf;
+#pragma unroll
+  for (int j = 0; j < kQK; ++j) {
+    if (t + j * kThreads < DK) {
+      s_q[t + j * kThreads] = qf[j];
+      s_k[t + j * kThreads] = kf[j];
+      sq += qf[j] * qf[j];
+      sk += kf[j] * kf[j];
+    }
   }
   sq = wave_sum(sq);
   sk = wave_sum(sk);
@@ -82,11 +94,9 @@ __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
     s_norm[1][wave] = sk;
   }
   // Gates (Qwen35HybridTextBackend.cpp:1091-1099), uniform per head.
-  const size_t gi = static_cast<size_t>(bseq) * Hv + hv;
-  const float beta = 1.0f / (1.0f + expf(-bf2f(bgate[gi])));
-  const float dtb = dt_bias ? bf2f(dt_bias[hv]) : 0.0f;
-  const float negA = A_log ? -expf(A_log[hv]) : -1.0f;
-  const float decay = expf(softplus_f(bf2f(a[gi]) + dtb) * negA);
+  const float beta = 1.0f / (1.0f + expf(-b_raw));
+  const float negA = A_log ? -expf(alog) : -1.0f;
+  const float decay = expf(softplus_f(a_raw + dtb) * negA);
   __syncthreads();
   const float qn = 1.0f / sqrtf(s_norm[0][0] + s_norm[0][1] + s_norm[0][2] + s_norm[0][3] + eps);
   const float kn = 1.0f / sqrtf(s_norm[1][0] + s_norm[1][1] + s_norm[1][2] + s_norm[1][3] + eps);
@@ -111,15 +121,11 @@ __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
       *reinterpret_cast<const f32x4*>(&s_red[0][3][cq * 4]);
 
   // 4. d = (v - u) * beta ; S += k d^T ; partial o = S^T q.
-  f32x4 vv = {0.f, 0.f, 0.f, 0.f};
-  if (active) {
-    const bf16* vh = v + gi * dv + col;
-    const uint2 raw = *reinterpret_cast<const uint2*>(vh);
-    vv[0] = __uint_as_float(raw.x << 16);
-    vv[1] = __uint_as_float(raw.x & 0xffff0000u);
-    vv[2] = __uint_as_float(raw.y << 16);
-    vv[3] = __uint_as_float(raw.y & 0xffff0000u);
-  }
+  f32x4 vv;
+  vv[0] = __uint_as_float(vraw.x << 16);
+  vv[1] = __uint_as_float(vraw.x & 0xffff0000u);
+  vv[2] = __uint_as_float(vraw.y << 16);
+  vv[3] = __uint_as_float(vraw.y & 0xffff0000u);
   const f32x4 d = (vv - u) * beta;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

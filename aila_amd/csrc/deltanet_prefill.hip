@@ -48,12 +48,6 @@ constexpr int kC = 64;          // chunk length
 constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;      // MI355X: 8 accelerator complex dies, one L2 each
 
-__device__ __forceinline__ float softplus_f(float x) {
-  if (x > 20.0f) return x;
-  if (x < -20.0f) return expf(x);
-  return log1pf(expf(x));
-}
-
 // Index held by slot e (0..7) of lane group g within a 32-wide k-step.
 __device__ __forceinline__ int slot_idx(int g, int e) { return (e < 4) ? 4 * g + e : 16 + 4 * g + (e - 4); }
 

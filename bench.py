@@ -61,6 +61,14 @@ def deltanet_bytes(B, Hk, Hv, dk, dv):
             + 2 * B * Hv * 2 + B * Hv * dv * 2)
 
 
+def deltanet_layer_bytes(B, Hk, Hv, d):
+    """Full layer step: state read + write, conv ring 3 rows read + 1 written
+    (fp32), the qkv row, z, a, b read, out written, conv_w read."""
+    ch = 2 * Hk * d + Hv * d
+    return (2 * B * Hv * d * d * 4 + 4 * B * ch * 4 + B * ch * 2 + B * Hv * d * 2 + 2 * B * Hv * 2
+            + B * Hv * d * 2 + ch * 4 * 2)
+
+
 def time_graph(torch, g, reps):
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -293,6 +301,55 @@ def sub_deltanet_decode(torch, aila_amd, steps=2048, per_graph=16):
             "GBps": round(byts / us / 1e3, 1), "x_of_state_traffic_bound": round(us / bound_us, 3)}
 
 
+def sub_deltanet_layer_decode(torch, aila_amd, steps=512, per_graph=16):
+    """Full layer decode (conv ring + SiLU + norms + recurrence + gated RMSNorm)
+    at the config-5 DeltaNet layer shape, next to the recurrence-only kernel
+    on the same state."""
+    B, Hk, Hv, d = B5, DN_HK, DN_HV, DN_D
+    ch = 2 * Hk * d + Hv * d
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 5)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    f32 = dict(dtype=torch.float32, device="cuda")
+    st = torch.empty((B, Hv, d, d), **f32).normal_(0, 0.02, generator=g)
+    cs = torch.empty((B, 3, ch), **f32).normal_(generator=g)
+    w = torch.randn((ch, 4), generator=g, **bf)
+    nw = torch.ones(d, **f32)
+    xs = [dict(qkv=torch.randn((B, ch), generator=g, **bf), z=torch.randn((B, Hv * d), generator=g, **bf),
+               a=torch.randn((B, Hv), generator=g, **bf), b=torch.randn((B, Hv), generator=g, **bf))
+          for _ in range(per_graph)]
+    out = torch.empty((B, Hv * d), **bf)
+    heads = torch.zeros((B,), dtype=torch.int32, device="cuda")
+    fn = lambda x: aila_amd.deltanet_layer_decode(x["qkv"], x["z"], x["a"], x["b"], w, cs, 0, nw, st, Hk,
+                                                  out=out, conv_heads=heads)
+    for x in xs:
+        fn(x)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for x in xs:
+            fn(x)
+    gr.replay()
+    us = time_graph(torch, gr, steps // per_graph) * 1e3 / per_graph
+    byts = deltanet_layer_bytes(B, Hk, Hv, d)
+    # the recurrence-only kernel on the same shape
+    q = [torch.randn((B, Hk, d), generator=g, **bf) for _ in range(2)]
+    v = torch.randn((B, Hv, d), generator=g, **bf)
+    o2 = torch.empty((B, Hv, d), **bf)
+    gr2 = torch.cuda.CUDAGraph()
+    aila_amd.deltanet_decode(q[0], q[1], v, xs[0]["a"], xs[0]["b"], st, out=o2)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gr2):
+        for _ in range(per_graph):
+            aila_amd.deltanet_decode(q[0], q[1], v, xs[0]["a"], xs[0]["b"], st, out=o2)
+    gr2.replay()
+    us2 = time_graph(torch, gr2, steps // per_graph) * 1e3 / per_graph
+    return {"config": f"layer decode B={B} Hk={Hk} Hv={Hv} d={d} (config-5 DeltaNet layer)",
+            "us_per_step": round(us, 3), "GBps": round(byts / us / 1e3, 1),
+            "x_of_bound": round(us / (byts / (HBM_PEAK_GBS * 1e3)), 3),
+            "recurrence_only_us": round(us2, 3)}
+
+
 def sub_deltanet_prefill(torch, aila_amd, reps=10):
     B, T, Hk, Hv, d = 1, 4096, 16, 32, 128
     g = torch.Generator(device="cuda")
@@ -321,6 +378,36 @@ def sub_deltanet_prefill(torch, aila_amd, reps=10):
     frac = max(byts / (HBM_PEAK_GBS * 1e9), flops / (BF16_PEAK_TFLOPS * 1e12)) / (us * 1e-6)
     return {"config": "4: T=4096 C=64 Hk=16 Hv=32 dk=dv=128", "us": round(us, 1),
             "tok_per_s": round(T / (us * 1e-6)), "roofline_frac": round(frac, 4)}
+
+
+def sub_decode_prep(torch, aila_amd, per_graph=32, reps=20):
+    """QK-norm + partial RoPE + packed q|gate split + K/V append for one
+    config-5 GQA layer (B=8, Hq=16, Hkv=4, D=256, rotary 64)."""
+    B, Hq, Hkv, D, rot = B5, GQA_HQ, GQA_HKV, GQA_D, 64
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 6)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    qg = torch.randn((B, Hq, 2 * D), generator=g, **bf)
+    k = torch.randn((B, Hkv, D), generator=g, **bf)
+    v = torch.randn((B, Hkv, D), generator=g, **bf)
+    wq, wk = torch.randn(D, generator=g, **bf), torch.randn(D, generator=g, **bf)
+    kc = torch.empty((B, Hkv, 1024, D), **bf)
+    vc = torch.empty_like(kc)
+    qo, go = torch.empty((B, Hq, D), **bf), torch.empty((B, Hq, D), **bf)
+    pos = torch.full((B,), 700, dtype=torch.int32, device="cuda")
+    fn = lambda: aila_amd.decode_prepare_qkv(qg, k, v, wq, wk, kc, vc, positions=pos, rotary_dim=rot,
+                                             theta=1e7, packed_gate=True, q_out=qo, gate_out=go)
+    fn()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for _ in range(per_graph):
+            fn()
+    gr.replay()
+    us = time_graph(torch, gr, reps) * 1e3 / per_graph
+    byts = B * Hq * 2 * D * 2 + 2 * B * Hq * D * 2 + 2 * B * Hkv * D * 2 + 3 * B * Hkv * D * 2
+    return {"config": f"decode prep B={B} Hq={Hq} Hkv={Hkv} D={D} rot={rot} packed q|gate",
+            "us_per_call": round(us, 2), "GBps": round(byts / us / 1e3, 1)}
 
 
 def sub_decode_cfg1(torch, aila_amd, per_graph=32, reps=20):
@@ -403,7 +490,8 @@ def main():
     ap.add_argument("--no-sub", action="store_true", help="skip the config 1-4 sub-metrics")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
-                    choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill"],
+                    choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill",
+                             "deltanet_layer_decode", "decode_prep"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     args = ap.parse_args()
@@ -418,9 +506,13 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
 
     if args.profile_kernel:
-        {"gqa_decode": profile_kernel, "gqa_prefill": lambda t, a: sub_prefill(t, a, reps=20),
+        r = {"gqa_decode": profile_kernel, "gqa_prefill": lambda t, a: sub_prefill(t, a, reps=20),
          "deltanet_decode": lambda t, a: sub_deltanet_decode(t, a, steps=320),
-         "deltanet_prefill": lambda t, a: sub_deltanet_prefill(t, a, reps=20)}[args.profile_kernel](torch, aila_amd)
+         "deltanet_prefill": lambda t, a: sub_deltanet_prefill(t, a, reps=20),
+         "deltanet_layer_decode": lambda t, a: sub_deltanet_layer_decode(t, a, steps=320),
+         "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20)}[args.profile_kernel](torch, aila_amd)
+        if r:
+            log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
         return
     log(f"[bench] config 5: {args.warmup} warmup + {args.steps} timed steps")
     r5 = bench_config5(torch, aila_amd, args.steps, args.warmup)
@@ -436,9 +528,13 @@ def main():
         log(f"[bench] prefill {sub['gqa_prefill']}")
         sub["deltanet_decode"] = sub_deltanet_decode(torch, aila_amd)
         log(f"[bench] deltanet decode {sub['deltanet_decode']}")
+        sub["deltanet_layer_decode"] = sub_deltanet_layer_decode(torch, aila_amd)
+        log(f"[bench] deltanet layer decode {sub['deltanet_layer_decode']}")
         sub["deltanet_prefill"] = sub_deltanet_prefill(torch, aila_amd)
         log(f"[bench] deltanet prefill {sub['deltanet_prefill']}")
         sub["gqa_decode_cfg1"] = sub_decode_cfg1(torch, aila_amd)
+        sub["decode_prep"] = sub_decode_prep(torch, aila_amd)
+        log(f"[bench] decode prep {sub['decode_prep']}")
         log(f"[bench] decode cfg1 {sub['gqa_decode_cfg1']}")
     cpu = None
     if not args.no_cpu:

@@ -145,6 +145,35 @@ int aila_hip_deltanet_decode(const void* q, const void* k, const void* v,
                              int dk, int dv, float eps, float scale,
                              void* stream);
 
+/* The whole Gated DeltaNet layer for one token per sequence, between the
+ * input projection and o_proj (the fast path of
+ * Qwen35HybridTextBackend::run_linear_delta_decode_gpu,
+ * src/models/Qwen35HybridTextBackend.cpp:1013-1166; host form :1640-1798):
+ *   qkv  row b at qkv + b*qkv_stride: [q (Hk*dk) | k (Hk*dk) | v (Hv*dv)] bf16
+ *   conv: y_c = silu(ring[h][c] w[c,0] + ring[h+1][c] w[c,1]
+ *                    + ring[h+2][c] w[c,2] + x_c w[c,3])   (rows mod 3)
+ *         then ring[h][c] = x_c, where h = conv_heads ? conv_heads[b] : conv_head;
+ *         conv_w [ch, 4] bf16; conv_state [B, 3, ch] fp32, ch = 2*Hk*dk + Hv*dv.
+ *         The caller advances the head by one per step (as :1162-1164 do).
+ *   recurrence: as aila_hip_deltanet_decode on the fp32 conv outputs;
+ *         a, b at a + b*ab_stride + hv (ab_stride = Hv for separate tensors,
+ *         the fused row width for the backend's [qkv | z | a | b] row).
+ *   gate: out[b, hv, :] = bf16(rmsnorm(o) * norm_w * silu(z)), rmsnorm over dv,
+ *         z row b at z + b*z_stride, norm_w [dv] fp32 (:1153-1160, :153-173).
+ * state [B, Hv, dk, dv] fp32 is read and written once. Supported: dk = dv =
+ * 128, conv kernel 4, Hv / Hk in {1, 2, 4} (the reference fast path's
+ * shapes). */
+int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride,
+                                   const void* z, int z_stride, const void* a,
+                                   const void* b, int ab_stride,
+                                   const void* conv_w, float* conv_state,
+                                   int conv_head, const int* conv_heads,
+                                   const void* dt_bias, const float* A_log,
+                                   const float* norm_w, float* state,
+                                   void* out, int B, int Hk, int Hv, int dk,
+                                   int dv, int conv_kernel, float eps,
+                                   float scale, void* stream);
+
 /* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W, U, P, K^T and
  * decay factors; about 72.8 KiB per (sequence, value head, 64-token chunk)).
  * 0 for unsupported shapes. */

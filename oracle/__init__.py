@@ -45,8 +45,8 @@ _SIGS = {
                                _I, _I, _I, _I, _I, _I, _F, _F, _I],
     "orc_deltanet_recurrent_f64": [_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _I, _I, _I, _I, _I, _I, _F, _F, _I],
-    "orc_deltanet_layer": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                           _I, _I, _I, _I, _I, _I, _I, _I, _F, _I],
+    "orc_deltanet_layer": [_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P,
+                           _I, _I, _I, _I, _I, _I, _I, _F, _F],
 }
 
 
@@ -203,6 +203,26 @@ def deltanet_recurrent(q, k, v, a, b, state, B, T, Hk, Hv, dk, dv, eps=1e-6,
                                      _p(st), _p(out), _p(outb), B, T, Hk, Hv, dk, dv, eps, scale,
                                      int(l2norm))
     return out, outb, st
+
+
+def deltanet_layer(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, state, B, T, Hk, Hv, dk, dv,
+                   K=4, eps=1e-6, scale=None, dt_bias=None, A_log=None, fast=False):
+    """Full layer: conv1d ring + SiLU, L2 norm, recurrence, gated RMSNorm.
+    qkv [B,T,2*Hk*dk+Hv*dv], z [B,T,Hv*dv], a/b [B,T,Hv] (uint16 bf16),
+    conv_w [ch,K] bf16, conv_state [B,K-1,ch] f32, norm_w [dv] f32.
+    Returns (out bf16 [B,T,Hv*dv], state_after, conv_state_after)."""
+    if scale is None:
+        scale = 1.0 / np.sqrt(dk)
+    qkv, z, a, b, conv_w = (_c(x, U16) for x in (qkv, z, a, b, conv_w))
+    dt_bias, A_log, norm_w = _c(dt_bias, U16), _c(A_log, F32), _c(norm_w, F32)
+    st = np.array(state, dtype=F32, copy=True, order="C")
+    cs = np.array(conv_state, dtype=F32, copy=True, order="C")
+    ch = 2 * Hk * dk + Hv * dv
+    out = np.zeros((B, T, Hv * dv), U16)
+    lib(fast).orc_deltanet_layer(_p(qkv), ch, _p(z), Hv * dv, _p(a), _p(b), Hv, _p(conv_w), _p(cs),
+                                 int(conv_head), _p(dt_bias), _p(A_log), _p(norm_w), _p(st), _p(out),
+                                 B, T, Hk, Hv, dk, dv, K, eps, scale)
+    return out, st, cs
 
 
 def deltanet_recurrent_f64(q, k, v, a, b, state, B, T, Hk, Hv, dk, dv, eps=1e-6,

@@ -524,8 +524,12 @@ static inline int key_head_for(int hv, int Hk, int Hv) {
 // (q,k [B,T,Hk,dk], v [B,T,Hv,dv], a,b [B,T,Hv]); dt_bias bf16 [Hv] and
 // A_log f32 [Hv] may be null (treated as 0). Outputs: o in f32 and/or bf16
 // [B,T,Hv,dv] (either may be null). R selects f32 (reference) or f64 (truth).
-template <typename R>
-static void deltanet_impl(const bf16_t* q, const bf16_t* k, const bf16_t* v,
+static inline float ld(bf16_t x) { return bf(x); }
+static inline float ld(float x) { return x; }
+
+// In = bf16_t (the op's bf16 inputs) or float (the layer's fp32 conv outputs).
+template <typename R, typename In = bf16_t>
+static void deltanet_impl(const In* q, const In* k, const In* v,
                           const bf16_t* a, const bf16_t* b,
                           const bf16_t* dt_bias, const float* A_log, R* state,
                           R* out, bf16_t* out_bf16, int B, int T, int Hk,
@@ -539,10 +543,10 @@ static void deltanet_impl(const bf16_t* q, const bf16_t* k, const bf16_t* v,
       std::vector<R> qf(dk), kf(dk), u(dv), dd(dv);
       for (int t = 0; t < T; ++t) {
         const size_t bt = static_cast<size_t>(bb) * T + t;
-        const bf16_t* qr = q + (bt * Hk + hk) * dk;
-        const bf16_t* kr = k + (bt * Hk + hk) * dk;
-        const bf16_t* vr = v + (bt * Hv + hv) * dv;
-        for (int j = 0; j < dk; ++j) { qf[j] = bf(qr[j]); kf[j] = bf(kr[j]); }
+        const In* qr = q + (bt * Hk + hk) * dk;
+        const In* kr = k + (bt * Hk + hk) * dk;
+        const In* vr = v + (bt * Hv + hv) * dv;
+        for (int j = 0; j < dk; ++j) { qf[j] = ld(qr[j]); kf[j] = ld(kr[j]); }
         if (l2norm) {
           R sq = 0, sk = 0;
           for (int j = 0; j < dk; ++j) { sq += qf[j] * qf[j]; sk += kf[j] * kf[j]; }
@@ -560,7 +564,7 @@ static void deltanet_impl(const bf16_t* q, const bf16_t* k, const bf16_t* v,
           R acc = 0;
           for (int j = 0; j < dk; ++j) acc += S[static_cast<size_t>(j) * dv + i] * kf[j];
           u[i] = acc;
-          dd[i] = (static_cast<R>(bf(vr[i])) - acc) * beta;
+          dd[i] = (static_cast<R>(ld(vr[i])) - acc) * beta;
         }
         for (int j = 0; j < dk; ++j) {                                  // :1760-1766
           R* row = S + static_cast<size_t>(j) * dv;
@@ -589,6 +593,71 @@ void orc_deltanet_recurrent(const bf16_t* q, const bf16_t* k, const bf16_t* v,
                             float scale, int l2norm) {
   deltanet_impl<float>(q, k, v, a, b, dt_bias, A_log, state, out, out_bf16, B,
                        T, Hk, Hv, dk, dv, eps, scale, l2norm);
+}
+
+// Full Gated DeltaNet layer core, following run_linear_delta_host
+// (Qwen35HybridTextBackend.cpp:1640-1798) with the device paths' conv ring
+// (:1013-1056 decode, :1376-1411 prefill):
+//   conv: per channel c of the [q | k | v] row (conv_ch = 2*Hk*dk + Hv*dv),
+//     y = silu(sum_{j<K-1} ring[(head + j) % (K-1)][c] * w[c*K + j]
+//              + x[c] * w[c*K + K-1])          (fp32, summed in that order)
+//     then ring[head][c] = x[c], head = (head + 1) % (K-1)
+//   recurrence on the fp32 conv outputs (deltanet_impl, l2norm on)
+//   gate: o <- o / sqrt(mean(o^2) + eps) * norm_w * silu(z)  per value head
+//     (head_rms_norm_and_silu_gate, :153-173), rounded to bf16.
+// Token rows: qkv at qkv + (b*T + t) * qkv_stride, z likewise with z_stride,
+// a and b with ab_stride (so the backend's fused [qkv | z | a | b] row is
+// qkv_stride = z_stride = ab_stride = its width). conv_w [conv_ch, K] bf16;
+// conv_state [B, K-1, conv_ch] fp32; norm_w [dv] fp32; out [B, T, Hv*dv].
+// The caller advances conv_head by T, as the backend does (:1502).
+void orc_deltanet_layer(const bf16_t* qkv, int qkv_stride, const bf16_t* z, int z_stride,
+                        const bf16_t* a, const bf16_t* b, int ab_stride, const bf16_t* conv_w,
+                        float* conv_state, int conv_head, const bf16_t* dt_bias, const float* A_log,
+                        const float* norm_w, float* state, bf16_t* out, int B, int T, int Hk, int Hv,
+                        int dk, int dv, int K, float eps, float scale) {
+  const int qd = Hk * dk, vd = Hv * dv, ch = 2 * qd + vd, R = K - 1;
+  const size_t BT = static_cast<size_t>(B) * T;
+  std::vector<float> qf(BT * qd), kf(BT * qd), vf(BT * vd), of(BT * vd);
+  std::vector<bf16_t> ag(BT * Hv), bg(BT * Hv);
+  auto silu = [](float x) { return x / (1.0f + std::exp(-x)); };
+  for (int bb = 0; bb < B; ++bb) {
+    float* ring = conv_state + static_cast<size_t>(bb) * R * ch;
+    int head = R > 0 ? ((conv_head % R) + R) % R : 0;
+    for (int t = 0; t < T; ++t) {
+      const size_t bt = static_cast<size_t>(bb) * T + t;
+      const bf16_t* x = qkv + bt * qkv_stride;
+      for (int c = 0; c < ch; ++c) {
+        const bf16_t* w = conv_w + static_cast<size_t>(c) * K;
+        float acc = 0.0f;
+        for (int j = 0; j < R; ++j) acc += ring[static_cast<size_t>((head + j) % R) * ch + c] * bf(w[j]);
+        acc += bf(x[c]) * bf(w[R]);
+        const float y = silu(acc);
+        if (c < qd) qf[bt * qd + c] = y;
+        else if (c < 2 * qd) kf[bt * qd + c - qd] = y;
+        else vf[bt * vd + c - 2 * qd] = y;
+      }
+      if (R > 0) {
+        for (int c = 0; c < ch; ++c) ring[static_cast<size_t>(head) * ch + c] = bf(x[c]);
+        head = (head + 1) % R;
+      }
+      for (int h = 0; h < Hv; ++h) {
+        ag[bt * Hv + h] = a[bt * ab_stride + h];
+        bg[bt * Hv + h] = b[bt * ab_stride + h];
+      }
+    }
+  }
+  deltanet_impl<float, float>(qf.data(), kf.data(), vf.data(), ag.data(), bg.data(), dt_bias, A_log, state,
+                              of.data(), nullptr, B, T, Hk, Hv, dk, dv, eps, scale, 1);
+  for (size_t bt = 0; bt < BT; ++bt)
+    for (int h = 0; h < Hv; ++h) {
+      const float* o = of.data() + (bt * Hv + h) * dv;
+      const bf16_t* zg = z + bt * z_stride + static_cast<size_t>(h) * dv;
+      float ss = 0.0f;
+      for (int i = 0; i < dv; ++i) ss += o[i] * o[i];
+      const float inv = 1.0f / std::sqrt(ss / static_cast<float>(dv) + eps);
+      for (int i = 0; i < dv; ++i)
+        out[(bt * Hv + h) * dv + i] = orc_f32_to_bf16(o[i] * inv * norm_w[i] * silu(bf(zg[i])));
+    }
 }
 
 void orc_deltanet_recurrent_f64(const bf16_t* q, const bf16_t* k,
