@@ -35,6 +35,9 @@ _SIGS = {
     "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_deltanet_prefill_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "aila_hip_deltanet_layer_prefill_workspace_size": ([_I, _I, _I, _I, _I, _I], _SZ),
+    "aila_hip_deltanet_layer_prefill": ([_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _SZ,
+                                         _I, _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_deltanet_layer_decode": ([_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P,
                                         _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_decode_prepare_qkv": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -326,6 +329,69 @@ def deltanet_layer_decode(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, s
         _ptr(conv_heads), _ptr(dt_bias), _ptr(A_log), _ptr(norm_w), _ptr(state), _ptr(out), B, Hk, Hv, dk, dv,
         K, float(eps), float(scale), _stream(stream))
     _check(rc, "aila_hip_deltanet_layer_decode")
+    return out
+
+
+def _tok_rows(t, dtype, B, T, width, name, align=2):
+    """A [B, T, width] view whose token rows may be strided (column slices of
+    fused rows); the rows of all sequences must be equally spaced."""
+    if t is None or not t.is_cuda or t.dtype != dtype:
+        raise ValueError(f"{name}: expected a {dtype} device tensor")
+    if t.dim() != 3 or tuple(t.shape) != (B, T, width) or (width > 1 and t.stride(2) != 1):
+        raise ValueError(f"{name}: shape {tuple(t.shape)} / strides {t.stride()}, expected [{B}, {T}, {width}]")
+    rs = t.stride(1) if T > 1 else (t.stride(0) if B > 1 else width)
+    if B > 1 and t.stride(0) != T * rs:
+        raise ValueError(f"{name}: sequences must follow each other (stride(0) = T * stride(1))")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name} must be {align}-byte aligned")
+    return rs
+
+
+def deltanet_layer_prefill_workspace_size(B: int, T: int, Hk: int, Hv: int, dk: int = 128, dv: int = 128) -> int:
+    return int(lib().aila_hip_deltanet_layer_prefill_workspace_size(B, T, Hk, Hv, dk, dv))
+
+
+def deltanet_layer_prefill(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, state, num_k_heads,
+                           out=None, workspace=None, dt_bias=None, A_log=None, eps: float = 1e-6,
+                           scale: float | None = None, stream=None):
+    """Full Gated DeltaNet layer over T tokens: qkv [B,T,ch], z [B,T,Hv*dv],
+    a/b [B,T,Hv] bf16 (token rows may be strided views of fused rows);
+    conv_state [B,3,ch] and state [B,Hv,dk,dv] fp32 updated in place.
+    Returns out [B,T,Hv*dv] bf16; the caller advances conv_head by T."""
+    import torch
+    B, Hv, dk, dv = state.shape
+    T = qkv.shape[1]
+    Hk = int(num_k_heads)
+    ch = 2 * Hk * dk + Hv * dv
+    qs = _tok_rows(qkv, torch.bfloat16, B, T, ch, "qkv", align=8)
+    zs = _tok_rows(z, torch.bfloat16, B, T, Hv * dv, "z", align=4)
+    ast = _tok_rows(a, torch.bfloat16, B, T, Hv, "a")
+    bst = _tok_rows(b, torch.bfloat16, B, T, Hv, "b")
+    if ast != bst:
+        raise ValueError("a and b must share one row stride")
+    K = conv_w.shape[1]
+    _need(conv_w, torch.bfloat16, (ch, K), "conv_w")
+    _need(conv_state, torch.float32, (B, K - 1, ch), "conv_state")
+    _need(norm_w, torch.float32, (dv,), "norm_w", align=8)
+    _need(state, torch.float32, (B, Hv, dk, dv), "state")
+    if dt_bias is not None:
+        _need(dt_bias, torch.bfloat16, (Hv,), "dt_bias", align=2)
+    if A_log is not None:
+        _need(A_log, torch.float32, (Hv,), "A_log", align=4)
+    if out is None:
+        out = torch.empty((B, T, Hv * dv), dtype=torch.bfloat16, device=state.device)
+    _need(out, torch.bfloat16, (B, T, Hv * dv), "out")
+    need = deltanet_layer_prefill_workspace_size(B, T, Hk, Hv, dk, dv)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=state.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(dk)
+    rc = lib().aila_hip_deltanet_layer_prefill(
+        _ptr(qkv), qs, _ptr(z), zs, _ptr(a), _ptr(b), ast, _ptr(conv_w), _ptr(conv_state), int(conv_head),
+        _ptr(dt_bias), _ptr(A_log), _ptr(norm_w), _ptr(state), _ptr(out), _ptr(workspace),
+        workspace.numel() * workspace.element_size(), B, T, Hk, Hv, dk, dv, K, float(eps), float(scale),
+        _stream(stream))
+    _check(rc, "aila_hip_deltanet_layer_prefill")
     return out
 
 

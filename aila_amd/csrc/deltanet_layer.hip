@@ -22,6 +22,14 @@
 #include "common.hpp"
 
 namespace aila {
+
+// Chunked prefill of the recurrence (deltanet_prefill.hip).
+size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split);
+void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* k_lo, const bf16* v_lo,
+                             const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
+                             float* state, bf16* out, unsigned char* records, int B, int T, int Hk, int Hv,
+                             float eps, float scale, hipStream_t st);
+
 namespace {
 
 constexpr int kD = 128;          // dk = dv = 128 (the reference fast path's shape)
@@ -185,8 +193,193 @@ __global__ __launch_bounds__(256 * G) void deltanet_layer_decode_kernel(
 
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
+// ---- prefill: causal conv + SiLU over T tokens into split planes ----------
+// Thread = 4 consecutive channels (never straddling the q/k/v boundaries,
+// all multiples of 4) over kConvTok consecutive tokens, with the three
+// previous raw rows in registers. History before token 0 is the ring:
+// h(-3) = ring[head], h(-2) = ring[head+1], h(-1) = ring[head+2].
+// Outputs: q as bf16; k and v as bf16 hi and bf16 residual lo planes, so
+// that hi + lo carries the fp32 activation to 2^-16 relative. The first
+// token block also writes the new ring (the last three raw rows, oldest at
+// row (head + T) % 3): it is the only block that reads or writes the ring.
+constexpr int kConvTok = 64;
+
+__global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
+    const bf16* __restrict__ qkv, int qkv_stride, const bf16* __restrict__ conv_w, float* __restrict__ conv_state,
+    int conv_head, bf16* __restrict__ q_hi, bf16* __restrict__ k_hi, bf16* __restrict__ k_lo,
+    bf16* __restrict__ v_hi, bf16* __restrict__ v_lo, int T, int qd, int vd) {
+  const int ch = 2 * qd + vd;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= ch) return;
+  const int b = blockIdx.z;
+  const int tb0 = blockIdx.y * kConvTok;
+  const int tend = min(T, tb0 + kConvTok);
+  const int head = ((conv_head % kRows) + kRows) % kRows;
+  const bf16* xb = qkv + static_cast<size_t>(b) * T * qkv_stride + c;
+  float* ring = conv_state + static_cast<size_t>(b) * kRows * ch + c;
+
+  // taps: w[c+i][j] for the 4 channels
+  const u32x4 w01 = *reinterpret_cast<const u32x4*>(conv_w + static_cast<size_t>(c) * kConvK);
+  const u32x4 w23 = *reinterpret_cast<const u32x4*>(conv_w + static_cast<size_t>(c) * kConvK + 8);
+  float w[4][4];
+  {
+    const uint32_t ww[8] = {w01[0], w01[1], w01[2], w01[3], w23[0], w23[1], w23[2], w23[3]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t word = ww[(i * 4 + j) >> 1];
+        w[i][j] = __uint_as_float(((i * 4 + j) & 1) ? (word & 0xffff0000u) : (word << 16));
+      }
+  }
+  auto load_x = [&](int t) __attribute__((always_inline)) {
+    const uint2 r = *reinterpret_cast<const uint2*>(xb + static_cast<size_t>(t) * qkv_stride);
+    return f32x4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                 __uint_as_float(r.y & 0xffff0000u)};
+  };
+  f32x4 old_ring[kRows];
+  auto hist = [&](int i) __attribute__((always_inline)) {   // raw row i (i >= -3)
+    return i < 0 ? old_ring[i + kRows] : load_x(i);
+  };
+  if (tb0 == 0) {
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) old_ring[j] = *reinterpret_cast<const f32x4*>(ring + static_cast<size_t>((head + j) % kRows) * ch);
+  }
+  f32x4 h0 = hist(tb0 - 3), h1 = hist(tb0 - 2), h2 = hist(tb0 - 1);
+  // destination plane and column
+  const bool is_q = c < qd, is_k = !is_q && c < 2 * qd;
+  const int width = (c < 2 * qd) ? qd : vd;
+  const int col = is_q ? c : (is_k ? c - qd : c - 2 * qd);
+  bf16* hi_plane = is_q ? q_hi : (is_k ? k_hi : v_hi);
+  bf16* lo_plane = is_k ? k_lo : v_lo;
+  for (int t = tb0; t < tend; ++t) {
+    const f32x4 x = load_x(t);
+    float y[4], r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float acc = h0[i] * w[i][0];
+      acc += h1[i] * w[i][1];
+      acc += h2[i] * w[i][2];
+      acc += x[i] * w[i][3];
+      y[i] = silu_f(acc);
+    }
+    const uint2 hw = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+    const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
+    *reinterpret_cast<uint2*>(hi_plane + o) = hw;
+    if (!is_q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t word = i < 2 ? hw.x : hw.y;
+        r[i] = y[i] - __uint_as_float((i & 1) ? (word & 0xffff0000u) : (word << 16));
+      }
+      *reinterpret_cast<uint2*>(lo_plane + o) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+    }
+    h0 = h1;
+    h1 = h2;
+    h2 = x;
+  }
+  if (tb0 == 0) {
+    // the ring after T tokens: raw rows T-3, T-2, T-1 at rows (head + T + j) % 3
+    f32x4 nr[kRows];
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) nr[j] = hist(T - kRows + j);
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) *reinterpret_cast<f32x4*>(ring + static_cast<size_t>((head + T + j) % kRows) * ch) = nr[j];
+  }
+}
+
+// ---- prefill epilogue: out = RMSNorm(o) * norm_w * SiLU(z), in place ------
+// One wave per (token, value head) row of 128 outputs, two per lane.
+__global__ __launch_bounds__(256) void deltanet_gate_kernel(bf16* __restrict__ out, const bf16* __restrict__ z,
+                                                            int z_stride, const float* __restrict__ norm_w,
+                                                            long rows, int Hv, float eps) {
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const long bt = row / Hv;
+  const int hv = static_cast<int>(row % Hv);
+  bf16* o = out + row * kD + lane * 2;
+  const uint32_t ow = *reinterpret_cast<const uint32_t*>(o);
+  const uint32_t zw = *reinterpret_cast<const uint32_t*>(z + bt * z_stride + hv * kD + lane * 2);
+  const f32x2 nw = *reinterpret_cast<const f32x2*>(norm_w + lane * 2);
+  const float o0 = __uint_as_float(ow << 16), o1 = __uint_as_float(ow & 0xffff0000u);
+  const float ss = wave_sum(o0 * o0 + o1 * o1);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+  const float r0 = o0 * inv * nw[0] * silu_f(__uint_as_float(zw << 16));
+  const float r1 = o1 * inv * nw[1] * silu_f(__uint_as_float(zw & 0xffff0000u));
+  *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(r0, r1);
+}
+
+struct LayerWs {   // byte offsets of the prefill workspace regions
+  size_t q_hi, k_hi, k_lo, v_hi, v_lo, records, total;
+};
+
+LayerWs layer_ws(int B, int T, int Hk, int Hv) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t qk = static_cast<size_t>(B) * T * Hk * kD * 2, vv = static_cast<size_t>(B) * T * Hv * kD * 2;
+  LayerWs w;
+  w.q_hi = 0;
+  w.k_hi = up(w.q_hi + qk);
+  w.k_lo = up(w.k_hi + qk);
+  w.v_hi = up(w.k_lo + qk);
+  w.v_lo = up(w.v_hi + vv);
+  w.records = up(w.v_lo + vv);
+  w.total = w.records + deltanet_chunk_records_bytes(B, T, Hv, true);
+  return w;
+}
+
 }  // namespace
+
 }  // namespace aila
+
+extern "C" size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk, int Hv, int dk, int dv) {
+  if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || dk != aila::kD || dv != aila::kD) return 0;
+  return aila::layer_ws(B, T, Hk, Hv).total;
+}
+
+extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, const void* z, int z_stride,
+                                               const void* a, const void* b, int ab_stride, const void* conv_w,
+                                               float* conv_state, int conv_head, const void* dt_bias,
+                                               const float* A_log, const float* norm_w, float* state, void* out,
+                                               void* workspace, size_t workspace_bytes, int B, int T, int Hk,
+                                               int Hv, int dk, int dv, int conv_kernel, float eps, float scale,
+                                               void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(qkv && z && a && b && conv_w && conv_state && norm_w && state && out,
+               "deltanet_layer_prefill: null pointer");
+  AILA_REQUIRE(dk == kD && dv == kD && conv_kernel == kConvK,
+               "deltanet_layer_prefill: needs dk = dv = 128 and conv kernel 4 (dk=%d dv=%d K=%d)", dk, dv,
+               conv_kernel);
+  AILA_REQUIRE(B > 0 && B <= 65535 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Hv <= 65535,
+               "deltanet_layer_prefill: bad shape (B=%d T=%d Hk=%d Hv=%d)", B, T, Hk, Hv);
+  const int qd = Hk * kD, vd = Hv * kD, ch = 2 * qd + vd;
+  AILA_REQUIRE(qkv_stride >= ch && z_stride >= vd && ab_stride >= Hv,
+               "deltanet_layer_prefill: row strides too small (qkv %d < %d, z %d, ab %d)", qkv_stride, ch, z_stride,
+               ab_stride);
+  AILA_REQUIRE(aligned(qkv, 8) && qkv_stride % 4 == 0 && aligned(conv_w, 16) && aligned(conv_state, 16) &&
+                   aligned(z, 4) && z_stride % 2 == 0 && aligned(norm_w, 8) && aligned(state, 16) &&
+                   aligned(out, 16),
+               "deltanet_layer_prefill: misaligned qkv/conv_w/conv_state/z/norm_w/state/out or odd strides");
+  const LayerWs w = layer_ws(B, T, Hk, Hv);
+  if (!workspace || workspace_bytes < w.total)
+    return set_error(AILA_HIP_EWORKSPACE, "deltanet_layer_prefill: workspace %zu < %zu bytes", workspace_bytes,
+                     w.total);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  auto plane = [&](size_t off) { return reinterpret_cast<bf16*>(ws + off); };
+  const dim3 cgrid((ch / 4 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
+  hipLaunchKernelGGL(deltanet_conv_split_kernel, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv), qkv_stride,
+                     static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi), plane(w.k_hi),
+                     plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
+  launch_deltanet_chunked(plane(w.q_hi), plane(w.k_hi), plane(w.v_hi), plane(w.k_lo), plane(w.v_lo),
+                          static_cast<const bf16*>(a), static_cast<const bf16*>(b), ab_stride,
+                          static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out), ws + w.records,
+                          B, T, Hk, Hv, eps, scale, st);
+  const long rows = static_cast<long>(B) * T * Hv;
+  hipLaunchKernelGGL(deltanet_gate_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st,
+                     static_cast<bf16*>(out), static_cast<const bf16*>(z), z_stride, norm_w, rows, Hv, eps);
+  return check_launch("deltanet_layer_prefill");
+}
 
 extern "C" int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride, const void* z, int z_stride,
                                               const void* a, const void* b, int ab_stride, const void* conv_w,

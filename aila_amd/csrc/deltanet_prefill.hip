@@ -19,9 +19,13 @@
 // All decays are formed as exp of differences with s <= t (never a ratio),
 // so they stay in [0, 1]. T is computed in fp32 (diagonal 16x16 blocks by
 // substitution, off-diagonal blocks on the fp32 matrix cores), the diagonal
-// of T is applied in fp32, and the state update K^T (fk D) uses a hi/lo bf16
-// split of (fk D); every other MFMA operand is either an exact bf16 input or
-// a single bf16 rounding.
+// of T is applied in fp32, and every product that feeds the state carries
+// its inexact operands as a hi + lo pair of bf16 (x = bf16(x) + bf16(x -
+// bf16(x)), 2^-16 relative): To diag(beta) and To diag(sw) in U and W, W and
+// S in D = U - W S, and (fk D) in the state update, each as hi*hi + hi*lo +
+// lo*hi. With decays near 1 the chunk's W S nearly cancels U, and single
+// bf16 roundings there would grow the state error past 1e-3 within a few
+// thousand tokens. The output-only products (Q S, P D) use single bf16.
 //
 // Kernel 1 (deltanet_chunk_prep_kernel): one workgroup per (chunk, value
 //   head, sequence), fully parallel, two per CU. K, Q, V tiles arrive by
@@ -72,25 +76,35 @@ __device__ __forceinline__ int swz_tr(int r) { return ((r & 7) << 1) | ((r >> 3)
 //   Q  [4 token tiles][4 k-steps][64][8 bf16]    Q[16w+l%16][32ks + slots of l/16]
 //   U  [DV/16 slabs][4 token tiles][64][4 f32]   C layout of U
 //   F  fq[C], fk[C], gamma (f32)
-template <int DK, int DV>
+//   WLo  the bf16 residual W - bf16(W), laid out as W
+//   KtLo (split inputs only) the bf16 residual K - bf16(K), laid out as Kt
+template <int DK, int DV, bool kLo = false>
 struct ChunkRec {
   static constexpr size_t kF = 0;
   static constexpr size_t kW = 1024;
-  static constexpr size_t kKt = kW + size_t(kC) * DK * 2;
+  static constexpr size_t kWLo = kW + size_t(kC) * DK * 2;
+  static constexpr size_t kKt = kWLo + size_t(kC) * DK * 2;
   static constexpr size_t kP = kKt + size_t(DK) * kC * 2;
   static constexpr size_t kQ = kP + size_t(kC) * kC * 2;
   static constexpr size_t kU = kQ + size_t(kC) * DK * 2;
-  static constexpr size_t kBytes = (kU + size_t(kC) * DV * 4 + 255) / 256 * 256;
+  static constexpr size_t kKtLo = kU + size_t(kC) * DV * 4;
+  static constexpr size_t kBytes = (kKtLo + (kLo ? size_t(DK) * kC * 2 : 0) + 255) / 256 * 256;
 };
 
 // ---------------------------------------------------------------------------
-template <int DK, int DV>
+// kLo: the inputs are fp32 values carried as bf16 hi planes (q, k, v) plus
+// bf16 residual planes (k_lo, v_lo). The residuals enter exactly where the
+// rounding of an input would reach the state beyond fp32 accuracy: the key
+// norms, U (its MFMA pass and diagonal term) and the K^T operand of the
+// state update (a KtLo record); K K^T, W, P and Q use the hi planes.
+template <int DK, int DV, bool kLo>
 __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const bf16* __restrict__ a, const bf16* __restrict__ bg, const bf16* __restrict__ dt_bias,
+    const bf16* __restrict__ k_lo, const bf16* __restrict__ v_lo,
+    const bf16* __restrict__ a, const bf16* __restrict__ bg, int ab_stride, const bf16* __restrict__ dt_bias,
     const float* __restrict__ A_log, unsigned char* __restrict__ ws, int T, int Hk, int Hv,
     float eps) {
-  using R = ChunkRec<DK, DV>;
+  using R = ChunkRec<DK, DV, kLo>;
   static_assert(DK == 128 && DV == 128, "tiles of 64 rows x 256 bytes");
   constexpr int RB = DK * 2;       // bytes per K/Q/V row
   constexpr int NC = DK / 8;       // 16-byte chunks per row
@@ -100,6 +114,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   __shared__ __attribute__((aligned(16))) float sT[kC * kC];              // To, fp32 [64][64]
   __shared__ __attribute__((aligned(16))) float sG2[kC], sGn[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
   float* sA = reinterpret_cast<float*>(sQA);
+  unsigned char* sKl = reinterpret_cast<unsigned char*>(sT);   // K residual (split inputs), steps 1-3
 
   const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
   const int nch = (T + kC - 1) / kC;
@@ -126,12 +141,23 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       dma16_to_lds(rq, r * kq_row + ((cc ^ swz_rows(r)) << 4), sQA + slot * 1024);
       dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
     }
+    if constexpr (kLo) {
+      // key residual tile into the To buffer, which is free until step 4
+      const u32x4 rl = buffer_rsrc(k_lo + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
+#pragma unroll
+      for (int i = 0; i < kC * NC / kThreads; ++i) {
+        const int slot = i * 4 + wave;
+        const int p = slot * 64 + lane;
+        const int r = p / NC, cc = p % NC;
+        dma16_to_lds(rl, r * kq_row + ((cc ^ swz_rows(r)) << 4), sKl + slot * 1024);
+      }
+    }
   }
   // gates of this chunk (wave 0, overlapping the DMA): beta, g, prefix sum G
   if (wave == 0) {
     float beta = 0.f, g = 0.f;
     if (lane < n) {
-      const size_t gi = (static_cast<size_t>(b) * T + t0 + lane) * Hv + hv;
+      const size_t gi = (static_cast<size_t>(b) * T + t0 + lane) * ab_stride + hv;
       beta = 1.0f / (1.0f + expf(-bf2f(bg[gi])));
       const float dtb = dt_bias ? bf2f(dt_bias[hv]) : 0.0f;
       const float negA = A_log ? -expf(A_log[hv]) : -1.0f;
@@ -157,6 +183,20 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   {
     const int r = tid >> 2, part = tid & 3;
     float sk = 0.f, sq = 0.f;
+    if constexpr (kLo) {
+      // |k|^2 of the fp32 key hi + lo
+      float hi[8], lo[8];
+#pragma unroll
+      for (int cc = 0; cc < NC / 4; ++cc) {
+        unpack8(row_chunk(sK, r, part * (NC / 4) + cc), hi);
+        unpack8(row_chunk(sKl, r, part * (NC / 4) + cc), lo);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = r < n ? hi[e] + lo[e] : 0.f;
+          sk = fmaf(x, x, sk);
+        }
+      }
+    }
 #pragma unroll
     for (int cc = 0; cc < NC / 4; ++cc) {
       float kf[8], qf[8];
@@ -164,7 +204,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       unpack8(row_chunk(sQA, r, part * (NC / 4) + cc), qf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        sk = fmaf(kf[e], kf[e], sk);
+        if constexpr (!kLo) sk = fmaf(kf[e], kf[e], sk);
         sq = fmaf(qf[e], qf[e], sq);
       }
     }
@@ -212,9 +252,15 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       while (tl > ti) { tl -= ti + 1; ++ti; }
       const int tj = tl;
 #pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks)
-        acc3[i][0] = mfma16x16x32(as_bf16x8(row_chunk(sK, ti * 16 + m16, ks * 4 + g4)),
-                                  as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4)), acc3[i][0]);
+      for (int ks = 0; ks < DK / 32; ++ks) {
+        const bf16x8_t ki = as_bf16x8(row_chunk(sK, ti * 16 + m16, ks * 4 + g4));
+        const bf16x8_t kj = as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4));
+        acc3[i][0] = mfma16x16x32(ki, kj, acc3[i][0]);
+        if constexpr (kLo) {
+          acc3[i][0] = mfma16x16x32(ki, as_bf16x8(row_chunk(sKl, tj * 16 + m16, ks * 4 + g4)), acc3[i][0]);
+          acc3[i][0] = mfma16x16x32(as_bf16x8(row_chunk(sKl, ti * 16 + m16, ks * 4 + g4)), kj, acc3[i][0]);
+        }
+      }
     } else if (job < 18) {
       const int ti = (job - 10) >> 1, s2 = (job - 10) & 1;
 #pragma unroll
@@ -329,22 +375,45 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
     __syncthreads();
   }
+  // Residual tiles by DMA into buffers whose contents are spent: V_lo into
+  // the A space (free once To is formed), later K_lo into the V space.
+  auto dma_tile = [&](const bf16* src_plane, int H, int hidx, bool trswz, unsigned char* dst) __attribute__((always_inline)) {
+    const int row = H * DK * 2;
+    const u32x4 rs = buffer_rsrc(src_plane + (static_cast<size_t>(b) * T + t0) * H * DK + hidx * DK, (n - 1) * row + RB);
+#pragma unroll
+    for (int i = 0; i < kC * NC / kThreads; ++i) {
+      const int slot = i * 4 + wave;
+      const int p = slot * 64 + lane;
+      const int r = p / NC, cc = p % NC;
+      dma16_to_lds(rs, r * row + ((cc ^ (trswz ? swz_tr(r) : swz_rows(r))) << 4), dst + slot * 1024);
+    }
+  };
+  if constexpr (kLo) {
+    dma_tile(v_lo, Hv, hv, true, sQA);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    __syncthreads();
+  }
 
   // ---- 5. U = bf16(To diag(beta)) V + diag(beta) V, then W likewise with K ----
   // wave w owns token tile w; A operands in slot order over s, B operands by
   // transposing reads of the V / K tiles in the same order.
   const int ti = wave;
   const int nks = ti / 2 + 1;                     // k-steps of 32 tokens up to the diagonal
-  auto a_operand = [&](int ks, const float* fac) __attribute__((always_inline)) {
+  // (To diag(fac)) in slot order as a hi + lo pair of bf16 operands
+  auto a_operand = [&](int ks, const float* fac, bf16x8_t& hi, bf16x8_t& lo) __attribute__((always_inline)) {
     const int t = ti * 16 + m16;
-    float f[8];
+    float f[8], r[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int s = ks * 32 + slot_idx(g4, e);
       f[e] = sT[t * kC + s] * fac[s];
     }
     const u32x4 w = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
-    return as_bf16x8(w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = f[e] - __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+    const u32x4 wl = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7])};
+    hi = as_bf16x8(w);
+    lo = as_bf16x8(wl);
   };
   auto b_operand = [&](const unsigned char* tile, bool trswz, int ks, int dt) __attribute__((always_inline)) {
     const int d = dt * 16 + 4 * (m16 & 3);
@@ -356,39 +425,57 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     return as_bf16x8(w);
   };
   {
-    bf16x8_t au[2];
+    bf16x8_t au[2], aul[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      if (ks < nks) au[ks] = a_operand(ks, sBeta);
+      if (ks < nks) a_operand(ks, sBeta, au[ks], aul[ks]);
     float* Uout = reinterpret_cast<float*>(rec + R::kU);
 #pragma unroll
     for (int dt = 0; dt < DV / 16; ++dt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        if (ks < nks) acc = mfma16x16x32(au[ks], b_operand(sVW, true, ks, dt), acc);
+        if (ks < nks) {
+          const bf16x8_t vb = b_operand(sVW, true, ks, dt);
+          acc = mfma16x16x32(au[ks], vb, acc);
+          acc = mfma16x16x32(aul[ks], vb, acc);
+          if constexpr (kLo) acc = mfma16x16x32(au[ks], b_operand(sQA, true, ks, dt), acc);
+        }
       // diagonal term: one transposing read gives V[ti*16 + 4*g4 + j][dt*16 + m16], j = 0..3
       const int vr = ti * 16 + 4 * g4 + (m16 >> 2), vd = dt * 16 + 4 * (m16 & 3);
-      const u32x2 vv = ds_read_tr4(sVW + vr * RB + (((vd >> 3) ^ swz_tr(vr)) << 4) + ((vd & 7) << 1));
+      const int voff = vr * RB + (((vd >> 3) ^ swz_tr(vr)) << 4) + ((vd & 7) << 1);
+      const u32x2 vv = ds_read_tr4(sVW + voff);
+      u32x2 vl = {0u, 0u};
+      if constexpr (kLo) vl = ds_read_tr4(sQA + voff);
       const f32x4 bt = v4(sBeta, ti * 16 + g4 * 4);
       f32x4 u;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        u[j] = acc[j] + bt[j] * __uint_as_float((j & 1) ? (vv[j >> 1] & 0xffff0000u) : (vv[j >> 1] << 16));
+      for (int j = 0; j < 4; ++j) {
+        float vf = __uint_as_float((j & 1) ? (vv[j >> 1] & 0xffff0000u) : (vv[j >> 1] << 16));
+        if constexpr (kLo) vf += __uint_as_float((j & 1) ? (vl[j >> 1] & 0xffff0000u) : (vl[j >> 1] << 16));
+        u[j] = acc[j] + bt[j] * vf;
+      }
       *reinterpret_cast<f32x4*>(&Uout[((dt * 4 + ti) * 64 + lane) * 4]) = u;   // C-layout order
     }
+  }
+  if constexpr (kLo) {
+    __syncthreads();                        // every wave is done with V
+    dma_tile(k_lo, Hk, hk, false, sVW);     // K residual again (its first copy was overwritten by To)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    __syncthreads();
   }
   // W^T (operands swapped: A = K^T by transposing reads, B = (To diag(sw))^T):
   // the C layout gives lane (g4, m16) W[t = 16*tile + m16][d = 16*dt + 4*g4 + j],
   // and d tiles 2*ks, 2*ks+1 together are its register-order slot of k-step ks.
   {
     const int t = ti * 16 + m16;
-    bf16x8_t bw[2];
+    bf16x8_t bw[2], bwl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      if (ks < nks) bw[ks] = a_operand(ks, sSw);
+      if (ks < nks) a_operand(ks, sSw, bw[ks], bwl[ks]);
     const float swt = sSw[t];
     u32x4* Wout = reinterpret_cast<u32x4*>(rec + R::kW);
+    u32x4* WLout = reinterpret_cast<u32x4*>(rec + R::kWLo);
 #pragma unroll
     for (int kso = 0; kso < DK / 32; ++kso) {
       float wv[8];
@@ -398,15 +485,32 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-          if (ks < nks) acc = mfma16x16x32(b_operand(sK, false, ks, dt), bw[ks], acc);
+          if (ks < nks) {
+            const bf16x8_t kb = b_operand(sK, false, ks, dt);
+            acc = mfma16x16x32(kb, bw[ks], acc);
+            acc = mfma16x16x32(kb, bwl[ks], acc);
+            if constexpr (kLo) acc = mfma16x16x32(b_operand(sVW, false, ks, dt), bw[ks], acc);
+          }
         const int d = dt * 16 + 4 * g4;
-        const u32x2 kk = *reinterpret_cast<const u32x2*>(sK + t * RB + (((d >> 3) ^ swz_rows(t)) << 4) + ((d & 7) << 1));
+        const int koff = t * RB + (((d >> 3) ^ swz_rows(t)) << 4) + ((d & 7) << 1);
+        const u32x2 kk = *reinterpret_cast<const u32x2*>(sK + koff);
+        u32x2 kl = {0u, 0u};
+        if constexpr (kLo) kl = *reinterpret_cast<const u32x2*>(sVW + koff);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          wv[4 * h + j] = acc[j] + swt * __uint_as_float((j & 1) ? (kk[j >> 1] & 0xffff0000u) : (kk[j >> 1] << 16));
+        for (int j = 0; j < 4; ++j) {
+          float kf = __uint_as_float((j & 1) ? (kk[j >> 1] & 0xffff0000u) : (kk[j >> 1] << 16));
+          if constexpr (kLo) kf += __uint_as_float((j & 1) ? (kl[j >> 1] & 0xffff0000u) : (kl[j >> 1] << 16));
+          wv[4 * h + j] = acc[j] + swt * kf;
+        }
       }
-      Wout[(ti * 4 + kso) * 64 + lane] = u32x4{pack_bf16x2(wv[0], wv[1]), pack_bf16x2(wv[2], wv[3]),
-                                               pack_bf16x2(wv[4], wv[5]), pack_bf16x2(wv[6], wv[7])};
+      const u32x4 wh = {pack_bf16x2(wv[0], wv[1]), pack_bf16x2(wv[2], wv[3]), pack_bf16x2(wv[4], wv[5]),
+                        pack_bf16x2(wv[6], wv[7])};
+      float wr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wr[e] = wv[e] - __uint_as_float((e & 1) ? (wh[e >> 1] & 0xffff0000u) : (wh[e >> 1] << 16));
+      Wout[(ti * 4 + kso) * 64 + lane] = wh;
+      WLout[(ti * 4 + kso) * 64 + lane] = u32x4{pack_bf16x2(wr[0], wr[1]), pack_bf16x2(wr[2], wr[3]),
+                                                pack_bf16x2(wr[4], wr[5]), pack_bf16x2(wr[6], wr[7])};
     }
   }
   // ---- 6. K^T in slot order over tokens, straight from transposing reads --------
@@ -419,6 +523,10 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int ks = job & 1, dt = job >> 1;
       const bf16x8_t op = b_operand(sK, false, ks, dt);   // K[tokens in slot order][dt*16 + m16]
       *reinterpret_cast<u32x4*>(&Ktout[((dt * 2 + ks) * 64 + lane) * 8]) = __builtin_bit_cast(u32x4, op);
+      if constexpr (kLo) {
+        const bf16x8_t ol = b_operand(sVW, false, ks, dt);
+        *reinterpret_cast<u32x4*>(rec + R::kKtLo + ((dt * 2 + ks) * 64 + lane) * 16) = __builtin_bit_cast(u32x4, ol);
+      }
     }
   }
   // ---- 7. row factors --------------------------------------------------------
@@ -435,7 +543,9 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
 // Per-chunk operands in registers (loaded two chunks ahead), by wave role.
 struct StateOps {
   u32x4 w[4];        // W rows of token tile w4, k-steps 0..3 (slot order)
+  u32x4 wl[4];       // residual of W
   u32x4 kt[2][2];    // K^T rows [key tile][token k-step]
+  u32x4 kt_lo[2][2]; // residual of K^T (split inputs only; unused and dropped otherwise)
   f32x4 u;           // U (C layout)
   f32x4 fk;          // fk of the 4 rows this lane holds
   float gam;
@@ -455,11 +565,11 @@ struct OutOps {
 // beside the state path; the chunk's two barriers order both:
 //   A: state: W S, D, publish D        | output: Q S (S of this chunk)
 //   B: state: K^T (fk D), publish S'   | output: + P D, store
-template <int DK, int DV>
+template <int DK, int DV, bool kLo>
 __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     const bf16* __restrict__ q, const unsigned char* __restrict__ ws, float* __restrict__ state,
     bf16* __restrict__ out, int T, int Hk, int Hv, float scale) {
-  using R = ChunkRec<DK, DV>;
+  using R = ChunkRec<DK, DV, kLo>;
   static_assert(DK == 4 * 32, "the four state waves own 32 key rows each");
   // XCD-aware placement: workgroups are dispatched round-robin over the 8
   // XCDs, so linear id i runs on XCD i % 8. All DV/16 slabs of one head are
@@ -483,6 +593,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
   const int col = slab * 16 + m16;
 
   __shared__ u32x4 sS[4][64];            // S B-operands, one per 32-row k-step
+  __shared__ u32x4 sSl[4][64];           // residual of S
   __shared__ u32x2 sD[2][2][64];         // D (bf16) B-operands: [k-step][half][lane]
   __shared__ u32x2 sDh[2][2][64];        // (fk D) hi
   __shared__ u32x2 sDl[2][2][64];        // (fk D) lo
@@ -497,11 +608,21 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       const u32x4* W = reinterpret_cast<const u32x4*>(rec + R::kW) + w4 * 4 * 64 + lane;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) o.w[ks] = W[ks * 64];
+      const u32x4* WL = reinterpret_cast<const u32x4*>(rec + R::kWLo) + w4 * 4 * 64 + lane;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) o.wl[ks] = WL[ks * 64];
       const u32x4* Kt = reinterpret_cast<const u32x4*>(rec + R::kKt) + lane;
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = Kt[((w4 * 2 + tt) * 2 + s2) * 64];
+      if constexpr (kLo) {
+        const u32x4* Ktl = reinterpret_cast<const u32x4*>(rec + R::kKtLo) + lane;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) o.kt_lo[tt][s2] = Ktl[((w4 * 2 + tt) * 2 + s2) * 64];
+      }
       o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + w4) * 64 + lane) * 16);
       const float* F = reinterpret_cast<const float*>(rec + R::kF);
       o.fk = *reinterpret_cast<const f32x4*>(F + kC + w4 * 16 + g4 * 4);
@@ -517,13 +638,25 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     auto publish_state = [&]() __attribute__((always_inline)) {
       const u32x4 w = {pack_bf16x2(s_reg[0][0], s_reg[0][1]), pack_bf16x2(s_reg[0][2], s_reg[0][3]),
                        pack_bf16x2(s_reg[1][0], s_reg[1][1]), pack_bf16x2(s_reg[1][2], s_reg[1][3])};
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        r[e] = s_reg[e >> 2][e & 3] - __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
       sS[w4][lane] = w;
+      sSl[w4][lane] = u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
+                            pack_bf16x2(r[6], r[7])};
     };
     auto chunk = [&](const StateOps& o, int cn, StateOps& on) __attribute__((always_inline)) {
-      // A: D = U - W S, published as bf16 and as hi/lo bf16 of fk D
+      // A: D = U - W S (hi*hi + hi*lo + lo*hi), published as bf16 and as
+      //    hi/lo bf16 of fk D
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks) acc = mfma16x16x32(as_bf16x8(o.w[ks]), as_bf16x8(sS[ks][lane]), acc);
+      for (int ks = 0; ks < DK / 32; ++ks) {
+        const bf16x8_t sh = as_bf16x8(sS[ks][lane]);
+        acc = mfma16x16x32(as_bf16x8(o.w[ks]), sh, acc);
+        acc = mfma16x16x32(as_bf16x8(o.w[ks]), as_bf16x8(sSl[ks][lane]), acc);
+        acc = mfma16x16x32(as_bf16x8(o.wl[ks]), sh, acc);
+      }
       {
         float dval[4], dsc[4], lo[4];
 #pragma unroll
@@ -551,6 +684,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
           const bf16x8_t aK = as_bf16x8(o.kt[tt][s2]);
           a2 = mfma16x16x32(aK, cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), a2);
           a2 = mfma16x16x32(aK, cat8x2(sDl[s2][0][lane], sDl[s2][1][lane]), a2);
+          if constexpr (kLo)
+            a2 = mfma16x16x32(as_bf16x8(o.kt_lo[tt][s2]), cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), a2);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) s_reg[tt][j] = o.gam * s_reg[tt][j] + a2[j];
@@ -632,10 +767,36 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
 }  // namespace
 }  // namespace aila
 
+namespace aila {
+// Chunk records + launches of the two kernels; shared by the recurrence
+// entry point (bf16 inputs) and the full layer (split fp32 inputs).
+size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split) {
+  const size_t nch = (static_cast<size_t>(T) + kC - 1) / kC;
+  return static_cast<size_t>(B) * Hv * nch * (split ? ChunkRec<128, 128, true>::kBytes : ChunkRec<128, 128, false>::kBytes);
+}
+
+void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* k_lo, const bf16* v_lo,
+                             const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
+                             float* state, bf16* out, unsigned char* records, int B, int T, int Hk, int Hv,
+                             float eps, float scale, hipStream_t st) {
+  const int nch = (T + kC - 1) / kC;
+  if (k_lo) {
+    hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128, true>), dim3(nch, Hv, B), dim3(kThreads), 0, st, q, k,
+                       v, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
+    hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128, true>), dim3(128 / 16, Hv, B), dim3(2 * kThreads), 0,
+                       st, q, records, state, out, T, Hk, Hv, scale);
+  } else {
+    hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128, false>), dim3(nch, Hv, B), dim3(kThreads), 0, st, q, k,
+                       v, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
+    hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128, false>), dim3(128 / 16, Hv, B), dim3(2 * kThreads), 0,
+                       st, q, records, state, out, T, Hk, Hv, scale);
+  }
+}
+}  // namespace aila
+
 extern "C" size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk, int dv) {
   if (B <= 0 || T <= 0 || Hv <= 0 || dk != 128 || dv != 128) return 0;
-  const size_t nch = (static_cast<size_t>(T) + aila::kC - 1) / aila::kC;
-  return static_cast<size_t>(B) * Hv * nch * aila::ChunkRec<128, 128>::kBytes;
+  return aila::deltanet_chunk_records_bytes(B, T, Hv, false);
 }
 
 extern "C" int aila_hip_deltanet_prefill(const void* q, const void* k, const void* v, const void* a,
@@ -652,15 +813,10 @@ extern "C" int aila_hip_deltanet_prefill(const void* q, const void* k, const voi
   const size_t need = aila_hip_deltanet_prefill_workspace_size(B, T, Hv, dk, dv);
   if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_prefill: workspace %zu < %zu bytes", workspace_bytes, need);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int nch = (T + kC - 1) / kC;
-  hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128>), dim3(nch, Hv, B), dim3(kThreads), 0, st,
-                     static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                     static_cast<const bf16*>(a), static_cast<const bf16*>(b),
-                     static_cast<const bf16*>(dt_bias), A_log, static_cast<unsigned char*>(workspace), T,
-                     Hk, Hv, eps);
-  hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128>), dim3(dv / 16, Hv, B), dim3(2 * kThreads), 0, st,
-                     static_cast<const bf16*>(q), static_cast<const unsigned char*>(workspace), state,
-                     static_cast<bf16*>(out), T, Hk, Hv, scale);
+  launch_deltanet_chunked(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                          nullptr, nullptr, static_cast<const bf16*>(a), static_cast<const bf16*>(b), Hv,
+                          static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out),
+                          static_cast<unsigned char*>(workspace), B, T, Hk, Hv, eps, scale,
+                          static_cast<hipStream_t>(stream));
   return check_launch("deltanet_prefill");
 }

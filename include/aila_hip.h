@@ -174,6 +174,37 @@ int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride,
                                    int dv, int conv_kernel, float eps,
                                    float scale, void* stream);
 
+/* Workspace bytes for aila_hip_deltanet_layer_prefill: the split conv
+ * outputs (q; k and v as bf16 hi + bf16 residual planes) and the chunk
+ * records with the key residual. 0 for unsupported shapes. */
+size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
+                                                      int Hv, int dk, int dv);
+
+/* The whole Gated DeltaNet layer over T tokens per sequence (the fast path
+ * of Qwen35HybridTextBackend::run_linear_delta_prefill_gpu_batched,
+ * src/models/Qwen35HybridTextBackend.cpp:1306-1508, which runs the decode
+ * step token by token; host form :1640-1798). Token t of sequence b reads
+ * qkv + (b*T + t)*qkv_stride, z + (b*T + t)*z_stride and a/b +
+ * (b*T + t)*ab_stride + hv (so the backend's fused [qkv | z | a | b] row is
+ * qkv = row, z = row + ch, a = row + ch + Hv*dv, b = a + Hv, every stride the
+ * row width). Same math as aila_hip_deltanet_layer_decode applied to the
+ * tokens in order, with the ring head advanced per token; the caller
+ * advances its head by T afterwards (:1502). The conv outputs stay fp32
+ * accurate into the recurrence (hi + lo bf16 planes); the recurrence runs
+ * chunked as aila_hip_deltanet_prefill. out [B, T, Hv*dv] bf16. Supported:
+ * dk = dv = 128, conv kernel 4, Hv % Hk == 0. */
+int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,
+                                    const void* z, int z_stride, const void* a,
+                                    const void* b, int ab_stride,
+                                    const void* conv_w, float* conv_state,
+                                    int conv_head, const void* dt_bias,
+                                    const float* A_log, const float* norm_w,
+                                    float* state, void* out, void* workspace,
+                                    size_t workspace_bytes, int B, int T,
+                                    int Hk, int Hv, int dk, int dv,
+                                    int conv_kernel, float eps, float scale,
+                                    void* stream);
+
 /* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W, U, P, K^T and
  * decay factors; about 72.8 KiB per (sequence, value head, 64-token chunk)).
  * 0 for unsupported shapes. */

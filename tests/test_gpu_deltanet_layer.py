@@ -129,3 +129,68 @@ def test_layer_decode_rejects_unsupported_shapes():
                                        torch.zeros((B, 3, ch), dtype=torch.float32, device="cuda"), 0,
                                        torch.ones(d, dtype=torch.float32, device="cuda"),
                                        torch.zeros((B, Hv, d, d), dtype=torch.float32, device="cuda"), Hk)
+
+
+# ------------------------------------------------------------------ prefill --
+def _slow_decay(x):
+    """Decays near 1 (exp(A_log) = 0.05, dt_bias = -3): the state remembers
+    hundreds of tokens, which is where input rounding would show."""
+    Hv = x["A_log"].shape[0]
+    return dict(x, A_log=np.full(Hv, np.log(0.05), np.float32),
+                dt_bias=dg.f32_to_bf16(np.full(Hv, -3.0, np.float32)))
+
+
+@pytest.mark.parametrize("B,T,Hk,Hv,head0,slow", [(2, 200, 2, 4, 1, False), (1, 1024, 16, 32, 0, False),
+                                                  (1, 1024, 2, 4, 2, True), (3, 64, 1, 1, 0, False),
+                                                  (1, 5, 2, 2, 2, False)])
+def test_layer_prefill_matches_oracle(B, T, Hk, Hv, head0, slow):
+    import torch
+    import aila_amd
+    x = _inputs(960 + T, B, T, Hk, Hv)
+    if slow:
+        x = _slow_decay(x)
+    want_out, want_S, want_cs = _oracle(x, B, T, Hk, Hv, head0)
+    st, cs = _t(x["state"]), _t(x["conv_state"])
+    print(f"layer prefill B={B} T={T} Hk={Hk} Hv={Hv} head0={head0} slow={slow}", flush=True)
+    out = aila_amd.deltanet_layer_prefill(_t(x["qkv"]), _t(x["z"]), _t(x["a"]), _t(x["b"]), _t(x["conv_w"]), cs,
+                                          head0, _t(x["norm_w"]), st, Hk, dt_bias=_t(x["dt_bias"]),
+                                          A_log=_t(x["A_log"]))
+    torch.cuda.synchronize()
+    e_s = _rel(_np(st), want_S)
+    e_o = _rel(dg.bf16_to_f32(_np(out)), dg.bf16_to_f32(want_out))
+    assert e_s <= STATE_TOL, f"state relerr {e_s}"
+    assert e_o <= OUT_TOL, f"out relerr {e_o}"
+    assert np.array_equal(_np(cs), want_cs), "conv ring must hold the last raw inputs bit-exact"
+
+
+def test_layer_prefill_fused_rows_then_decode():
+    """Prefill from the backend's fused [qkv | z | a | b] rows, then decode
+    steps continuing the same ring and state; all against one oracle run."""
+    import torch
+    import aila_amd
+    B, Hk, Hv, T0, steps, d = 2, 2, 4, 130, 4, 128
+    T = T0 + steps
+    x = _inputs(990, B, T, Hk, Hv)
+    head0 = 2
+    want_out, want_S, want_cs = _oracle(x, B, T, Hk, Hv, head0)
+    ch, zd = 2 * Hk * d + Hv * d, Hv * d
+    fused = np.concatenate([x["qkv"], x["z"], x["a"], x["b"]], axis=2)      # [B, T, all_dim]
+    fp = _t(fused[:, :T0])        # the prefill forward's rows, then one row buffer per decode step
+    f = _t(fused)
+    st, cs = _t(x["state"]), _t(x["conv_state"])
+    w, nw, dtb, alog = _t(x["conv_w"]), _t(x["norm_w"]), _t(x["dt_bias"]), _t(x["A_log"])
+    o_pre = aila_amd.deltanet_layer_prefill(fp[:, :, :ch], fp[:, :, ch:ch + zd], fp[:, :, ch + zd:ch + zd + Hv],
+                                            fp[:, :, ch + zd + Hv:], w, cs, head0, nw, st, Hk, dt_bias=dtb,
+                                            A_log=alog)
+    outs = [o_pre]
+    for t in range(T0, T):
+        row = f[:, t]
+        o = aila_amd.deltanet_layer_decode(row[:, :ch], row[:, ch:ch + zd], row[:, ch + zd:ch + zd + Hv],
+                                           row[:, ch + zd + Hv:], w, cs, (head0 + t) % 3, nw, st, Hk,
+                                           dt_bias=dtb, A_log=alog)
+        outs.append(o[:, None])
+    torch.cuda.synchronize()
+    got = np.concatenate([_np(o) for o in outs], axis=1)
+    assert _rel(_np(st), want_S) <= STATE_TOL
+    assert _rel(dg.bf16_to_f32(got), dg.bf16_to_f32(want_out)) <= OUT_TOL
+    assert np.array_equal(_np(cs), want_cs)

@@ -106,3 +106,31 @@ def test_prefill_rejects_bad_args():
     st = torch.zeros((1, 2, 64, 64), dtype=torch.float32, device="cuda")
     with pytest.raises(aila_amd.AilaHipError):
         aila_amd.deltanet_prefill(q, q, v, ab, ab, st)     # dk = 64 unsupported
+
+
+@pytest.mark.parametrize("decay", [0.9, 0.99, 0.999])
+def test_prefill_slow_decays_keep_state_accuracy(decay):
+    """Decays near 1 (long-memory heads): the chunk's W S nearly cancels U,
+    so the state error is most sensitive to operand rounding here. A_log is
+    set so that exp(-softplus(a + dt_bias) * exp(A_log)) ~ decay at a = 0."""
+    import torch
+    import aila_amd
+    B, T, H, d = 1, 2048, 4, 128
+    dtb_v = -4.0
+    alog = np.full(H, np.log(-np.log(decay) / np.log1p(np.exp(dtb_v))), np.float32)
+    dtb = dg.f32_to_bf16(np.full(H, dtb_v, np.float32))
+    q = dg.normal_bf16(801, 0, (B, T, H, d))
+    k = dg.normal_bf16(801, 1, (B, T, H, d))
+    v = dg.normal_bf16(801, 2, (B, T, H, d))
+    a = dg.normal_bf16(801, 3, (B, T, H), std=0.3)
+    b = dg.normal_bf16(801, 4, (B, T, H))
+    S0 = np.zeros((B, H, d, d), np.float32)
+    st = _t(S0)
+    out = aila_amd.deltanet_prefill(_t(q), _t(k), _t(v), _t(a), _t(b), st, dt_bias=_t(dtb), A_log=_t(alog))
+    torch.cuda.synchronize()
+    _, want_ob, want_S = oracle.deltanet_recurrent(q, k, v, a, b, S0, B, T, H, H, d, d, dt_bias=dtb, A_log=alog,
+                                                   fast=True)
+    es = _relerr(st.cpu().numpy(), want_S)
+    eo = _relerr(dg.bf16_to_f32(_np(out)), dg.bf16_to_f32(want_ob))
+    assert es <= STATE_TOL, f"state relerr {es}"
+    assert eo <= OUT_TOL, f"out relerr {eo}"
