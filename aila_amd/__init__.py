@@ -364,7 +364,7 @@ def deltanet_layer_prefill(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, 
     Hk = int(num_k_heads)
     ch = 2 * Hk * dk + Hv * dv
     qs = _tok_rows(qkv, torch.bfloat16, B, T, ch, "qkv", align=8)
-    zs = _tok_rows(z, torch.bfloat16, B, T, Hv * dv, "z", align=4)
+    zs = _tok_rows(z, torch.bfloat16, B, T, Hv * dv, "z", align=16)
     ast = _tok_rows(a, torch.bfloat16, B, T, Hv, "a")
     bst = _tok_rows(b, torch.bfloat16, B, T, Hv, "b")
     if ast != bst:
@@ -372,7 +372,7 @@ def deltanet_layer_prefill(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, 
     K = conv_w.shape[1]
     _need(conv_w, torch.bfloat16, (ch, K), "conv_w")
     _need(conv_state, torch.float32, (B, K - 1, ch), "conv_state")
-    _need(norm_w, torch.float32, (dv,), "norm_w", align=8)
+    _need(norm_w, torch.float32, (dv,), "norm_w", align=16)
     _need(state, torch.float32, (B, Hv, dk, dv), "state")
     if dt_bias is not None:
         _need(dt_bias, torch.bfloat16, (Hv,), "dt_bias", align=2)

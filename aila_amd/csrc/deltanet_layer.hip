@@ -202,7 +202,8 @@ bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) %
 // that hi + lo carries the fp32 activation to 2^-16 relative. The first
 // token block also writes the new ring (the last three raw rows, oldest at
 // row (head + T) % 3): it is the only block that reads or writes the ring.
-constexpr int kConvTok = 64;
+constexpr int kConvTok = 32;
+constexpr int kConvBatch = 8;   // rows loaded together before they are used
 
 __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
     const bf16* __restrict__ qkv, int qkv_stride, const bf16* __restrict__ conv_w, float* __restrict__ conv_state,
@@ -252,31 +253,40 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
   const int col = is_q ? c : (is_k ? c - qd : c - 2 * qd);
   bf16* hi_plane = is_q ? q_hi : (is_k ? k_hi : v_hi);
   bf16* lo_plane = is_k ? k_lo : v_lo;
-  for (int t = tb0; t < tend; ++t) {
-    const f32x4 x = load_x(t);
-    float y[4], r[4];
+  for (int tb = tb0; tb < tend; tb += kConvBatch) {
+    // a batch of rows in flight at once (clamped, so the loads stay unconditional)
+    f32x4 xs[kConvBatch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float acc = h0[i] * w[i][0];
-      acc += h1[i] * w[i][1];
-      acc += h2[i] * w[i][2];
-      acc += x[i] * w[i][3];
-      y[i] = silu_f(acc);
-    }
-    const uint2 hw = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-    const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
-    *reinterpret_cast<uint2*>(hi_plane + o) = hw;
-    if (!is_q) {
+    for (int i = 0; i < kConvBatch; ++i) xs[i] = load_x(min(tb + i, T - 1));
+#pragma unroll
+    for (int u = 0; u < kConvBatch; ++u) {
+      const int t = tb + u;
+      if (t >= tend) break;
+      const f32x4 x = xs[u];
+      float y[4], r[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t word = i < 2 ? hw.x : hw.y;
-        r[i] = y[i] - __uint_as_float((i & 1) ? (word & 0xffff0000u) : (word << 16));
+        float acc = h0[i] * w[i][0];
+        acc += h1[i] * w[i][1];
+        acc += h2[i] * w[i][2];
+        acc += x[i] * w[i][3];
+        y[i] = silu_f(acc);
       }
-      *reinterpret_cast<uint2*>(lo_plane + o) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+      const uint2 hw = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
+      *reinterpret_cast<uint2*>(hi_plane + o) = hw;
+      if (!is_q) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t word = i < 2 ? hw.x : hw.y;
+          r[i] = y[i] - __uint_as_float((i & 1) ? (word & 0xffff0000u) : (word << 16));
+        }
+        *reinterpret_cast<uint2*>(lo_plane + o) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+      }
+      h0 = h1;
+      h1 = h2;
+      h2 = x;
     }
-    h0 = h1;
-    h1 = h2;
-    h2 = x;
   }
   if (tb0 == 0) {
     // the ring after T tokens: raw rows T-3, T-2, T-1 at rows (head + T + j) % 3
@@ -289,25 +299,44 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
 }
 
 // ---- prefill epilogue: out = RMSNorm(o) * norm_w * SiLU(z), in place ------
-// One wave per (token, value head) row of 128 outputs, two per lane.
+// A (token, value head) row of 128 outputs per 16 lanes (8 per lane, one
+// 16-byte access each); kGateRows rows per 256-thread block.
+constexpr int kGateRows = 16 * 2;
 __global__ __launch_bounds__(256) void deltanet_gate_kernel(bf16* __restrict__ out, const bf16* __restrict__ z,
                                                             int z_stride, const float* __restrict__ norm_w,
                                                             long rows, int Hv, float eps) {
-  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int lane = threadIdx.x & 63;
-  const long bt = row / Hv;
-  const int hv = static_cast<int>(row % Hv);
-  bf16* o = out + row * kD + lane * 2;
-  const uint32_t ow = *reinterpret_cast<const uint32_t*>(o);
-  const uint32_t zw = *reinterpret_cast<const uint32_t*>(z + bt * z_stride + hv * kD + lane * 2);
-  const f32x2 nw = *reinterpret_cast<const f32x2*>(norm_w + lane * 2);
-  const float o0 = __uint_as_float(ow << 16), o1 = __uint_as_float(ow & 0xffff0000u);
-  const float ss = wave_sum(o0 * o0 + o1 * o1);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
-  const float r0 = o0 * inv * nw[0] * silu_f(__uint_as_float(zw << 16));
-  const float r1 = o1 * inv * nw[1] * silu_f(__uint_as_float(zw & 0xffff0000u));
-  *reinterpret_cast<uint32_t*>(o) = pack_bf16x2(r0, r1);
+  const int sub = threadIdx.x & 15;
+  const f32x4 nw0 = *reinterpret_cast<const f32x4*>(norm_w + sub * 8);
+  const f32x4 nw1 = *reinterpret_cast<const f32x4*>(norm_w + sub * 8 + 4);
+  const float nw[8] = {nw0[0], nw0[1], nw0[2], nw0[3], nw1[0], nw1[1], nw1[2], nw1[3]};
+  u32x4 ov[2], zv[2];
+  long rowv[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {   // both rows' loads first
+    const long row = static_cast<long>(blockIdx.x) * kGateRows + k * 16 + (threadIdx.x >> 4);
+    rowv[k] = row;
+    const long rr = row < rows ? row : rows - 1;
+    const long bt = rr / Hv;
+    const int hv = static_cast<int>(rr % Hv);
+    ov[k] = ld16(out + rr * kD + sub * 8);
+    zv[k] = ld16(z + bt * z_stride + hv * kD + sub * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    float o[8], zf[8], r[8];
+    unpack8(ov[k], o);
+    unpack8(zv[k], zf);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(o[e], o[e], ss);
+    ss = row16_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = o[e] * inv * nw[e] * silu_f(zf[e]);
+    if (rowv[k] < rows)
+      *reinterpret_cast<u32x4*>(out + rowv[k] * kD + sub * 8) =
+          u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]), pack_bf16x2(r[6], r[7])};
+  }
 }
 
 struct LayerWs {   // byte offsets of the prefill workspace regions
@@ -357,7 +386,7 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
                "deltanet_layer_prefill: row strides too small (qkv %d < %d, z %d, ab %d)", qkv_stride, ch, z_stride,
                ab_stride);
   AILA_REQUIRE(aligned(qkv, 8) && qkv_stride % 4 == 0 && aligned(conv_w, 16) && aligned(conv_state, 16) &&
-                   aligned(z, 4) && z_stride % 2 == 0 && aligned(norm_w, 8) && aligned(state, 16) &&
+                   aligned(z, 16) && z_stride % 8 == 0 && aligned(norm_w, 16) && aligned(state, 16) &&
                    aligned(out, 16),
                "deltanet_layer_prefill: misaligned qkv/conv_w/conv_state/z/norm_w/state/out or odd strides");
   const LayerWs w = layer_ws(B, T, Hk, Hv);
@@ -376,7 +405,7 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
                           static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out), ws + w.records,
                           B, T, Hk, Hv, eps, scale, st);
   const long rows = static_cast<long>(B) * T * Hv;
-  hipLaunchKernelGGL(deltanet_gate_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st,
+  hipLaunchKernelGGL(deltanet_gate_kernel, dim3(static_cast<unsigned>((rows + kGateRows - 1) / kGateRows)), dim3(256), 0, st,
                      static_cast<bf16*>(out), static_cast<const bf16*>(z), z_stride, norm_w, rows, Hv, eps);
   return check_launch("deltanet_layer_prefill");
 }
