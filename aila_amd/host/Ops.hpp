@@ -127,5 +127,30 @@ void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Ten
                                         int text_pos_delta = 0, int mrope_section_t = 0,
                                         int mrope_section_h = 0, int mrope_section_w = 0);
 
+// ---- the whole Gated DeltaNet layer (conv ring, norms, recurrence, gate) ----
+// Qwen35HybridTextBackend::run_linear_delta_decode_gpu (:975-1166) as a free
+// function: qkv [1, 2*Hk*dk + Hv*dv], z [1, Hv*dv], a/b [1, Hv] bf16;
+// conv1d_weight [conv_ch, conv_kernel] bf16 (Layer::linear_conv1d_weight);
+// conv_state [conv_kernel-1, conv_ch] fp32 and state [Hv, dk, dv] fp32
+// (LayerCache::linear_conv_state / linear_state) updated in place;
+// norm_weight [dv] fp32; out [1, Hv*dv] bf16. conv_head is the cache's
+// linear_conv_head and is advanced by one, as the backend does (:1163).
+// scale = 1/sqrt(head_k_dim) as in the backend (:991).
+void linear_delta_layer_decode(Context& ctx, Tensor& qkv, Tensor& z, Tensor& a, Tensor& b, Tensor& conv1d_weight,
+                               Tensor& conv_state, int& conv_head, Tensor* dt_bias, Tensor* A_log,
+                               Tensor& norm_weight, Tensor& state, Tensor& out, int num_k_heads, int num_v_heads,
+                               int head_k_dim, int head_v_dim, int conv_kernel, float eps);
+
+// run_linear_delta_prefill_gpu_batched (:1306-1508): fused_all [seq_len,
+// all_dim] rows of [qkv | z | a | b] (all_dim = conv_ch + Hv*dv + 2*Hv),
+// out [seq_len, Hv*dv]; conv_head advanced by seq_len (:1506). workspace u8
+// of at least linear_delta_layer_prefill_workspace_bytes(...).
+size_t linear_delta_layer_prefill_workspace_bytes(int seq_len, int num_k_heads, int num_v_heads, int head_k_dim,
+                                                  int head_v_dim);
+void linear_delta_layer_prefill(Context& ctx, Tensor& fused_all, Tensor& out, int seq_len, Tensor& conv1d_weight,
+                                Tensor& conv_state, int& conv_head, Tensor* dt_bias, Tensor* A_log,
+                                Tensor& norm_weight, Tensor& state, Tensor& workspace, int num_k_heads,
+                                int num_v_heads, int head_k_dim, int head_v_dim, int conv_kernel, float eps);
+
 }  // namespace ops
 }  // namespace aila

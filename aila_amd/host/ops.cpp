@@ -2,6 +2,7 @@
 #include "Ops.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <stdexcept>
 #include <string>
 
@@ -226,6 +227,51 @@ void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Ten
                                     num_heads_q, num_kv_heads, head_dim, static_cast<int>(k_cache.shape(1)),
                                     rotary_dim, theta, eps, start_pos, nullptr, ctx.stream()),
         "decode_prepare_qgkv_packed_partial");
+}
+
+void linear_delta_layer_decode(Context& ctx, Tensor& qkv, Tensor& z, Tensor& a, Tensor& b, Tensor& conv1d_weight,
+                               Tensor& conv_state, int& conv_head, Tensor* dt_bias, Tensor* A_log,
+                               Tensor& norm_weight, Tensor& state, Tensor& out, int num_k_heads, int num_v_heads,
+                               int head_k_dim, int head_v_dim, int conv_kernel, float eps) {
+  for (Tensor* t : {&qkv, &z, &a, &b, &conv1d_weight, &out}) need_dtype(*t, DType::bf16, "linear_delta_layer_decode");
+  for (Tensor* t : {&conv_state, &state, &norm_weight}) need_dtype(*t, DType::f32, "linear_delta_layer_decode");
+  const int ch = 2 * num_k_heads * head_k_dim + num_v_heads * head_v_dim;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(head_k_dim));
+  check(aila_hip_deltanet_layer_decode(qkv.data(), ch, z.data(), num_v_heads * head_v_dim, a.data(), b.data(),
+                                       num_v_heads, conv1d_weight.data(), conv_state.data_as<float>(), conv_head,
+                                       nullptr, dt_bias ? dt_bias->data() : nullptr,
+                                       A_log ? A_log->data_as<float>() : nullptr, norm_weight.data_as<float>(),
+                                       state.data_as<float>(), out.data(), 1, num_k_heads, num_v_heads, head_k_dim,
+                                       head_v_dim, conv_kernel, eps, scale, ctx.stream()),
+        "linear_delta_layer_decode");
+  if (conv_kernel > 1) conv_head = (conv_head + 1) % (conv_kernel - 1);
+}
+
+size_t linear_delta_layer_prefill_workspace_bytes(int seq_len, int num_k_heads, int num_v_heads, int head_k_dim,
+                                                  int head_v_dim) {
+  return aila_hip_deltanet_layer_prefill_workspace_size(1, seq_len, num_k_heads, num_v_heads, head_k_dim,
+                                                        head_v_dim);
+}
+
+void linear_delta_layer_prefill(Context& ctx, Tensor& fused_all, Tensor& out, int seq_len, Tensor& conv1d_weight,
+                                Tensor& conv_state, int& conv_head, Tensor* dt_bias, Tensor* A_log,
+                                Tensor& norm_weight, Tensor& state, Tensor& workspace, int num_k_heads,
+                                int num_v_heads, int head_k_dim, int head_v_dim, int conv_kernel, float eps) {
+  for (Tensor* t : {&fused_all, &conv1d_weight, &out}) need_dtype(*t, DType::bf16, "linear_delta_layer_prefill");
+  for (Tensor* t : {&conv_state, &state, &norm_weight}) need_dtype(*t, DType::f32, "linear_delta_layer_prefill");
+  const int ch = 2 * num_k_heads * head_k_dim + num_v_heads * head_v_dim;
+  const int zd = num_v_heads * head_v_dim;
+  const int all_dim = ch + zd + 2 * num_v_heads;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(head_k_dim));
+  uint16_t* row = fused_all.data_as<uint16_t>();
+  check(aila_hip_deltanet_layer_prefill(row, all_dim, row + ch, all_dim, row + ch + zd, row + ch + zd + num_v_heads,
+                                        all_dim, conv1d_weight.data(), conv_state.data_as<float>(), conv_head,
+                                        dt_bias ? dt_bias->data() : nullptr, A_log ? A_log->data_as<float>() : nullptr,
+                                        norm_weight.data_as<float>(), state.data_as<float>(), out.data(),
+                                        workspace.data(), workspace.size_bytes(), 1, seq_len, num_k_heads,
+                                        num_v_heads, head_k_dim, head_v_dim, conv_kernel, eps, scale, ctx.stream()),
+        "linear_delta_layer_prefill");
+  if (conv_kernel > 1) conv_head = (conv_head + seq_len) % (conv_kernel - 1);
 }
 
 }  // namespace ops

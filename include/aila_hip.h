@@ -154,7 +154,7 @@ int aila_hip_deltanet_decode(const void* q, const void* k, const void* v,
  *                    + ring[h+2][c] w[c,2] + x_c w[c,3])   (rows mod 3)
  *         then ring[h][c] = x_c, where h = conv_heads ? conv_heads[b] : conv_head;
  *         conv_w [ch, 4] bf16; conv_state [B, 3, ch] fp32, ch = 2*Hk*dk + Hv*dv.
- *         The caller advances the head by one per step (as :1162-1164 do).
+ *         The caller advances the head by one per step (as :1163 does).
  *   recurrence: as aila_hip_deltanet_decode on the fp32 conv outputs;
  *         a, b at a + b*ab_stride + hv (ab_stride = Hv for separate tensors,
  *         the fused row width for the backend's [qkv | z | a | b] row).
@@ -189,7 +189,7 @@ size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
  * qkv = row, z = row + ch, a = row + ch + Hv*dv, b = a + Hv, every stride the
  * row width). Same math as aila_hip_deltanet_layer_decode applied to the
  * tokens in order, with the ring head advanced per token; the caller
- * advances its head by T afterwards (:1502). The conv outputs stay fp32
+ * advances its head by T afterwards (:1506). The conv outputs stay fp32
  * accurate into the recurrence (hi + lo bf16 planes); the recurrence runs
  * chunked as aila_hip_deltanet_prefill. out [B, T, Hv*dv] bf16. Supported:
  * dk = dv = 128, conv kernel 4, Hv % Hk == 0. */

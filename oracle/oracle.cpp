@@ -609,7 +609,7 @@ void orc_deltanet_recurrent(const bf16_t* q, const bf16_t* k, const bf16_t* v,
 // a and b with ab_stride (so the backend's fused [qkv | z | a | b] row is
 // qkv_stride = z_stride = ab_stride = its width). conv_w [conv_ch, K] bf16;
 // conv_state [B, K-1, conv_ch] fp32; norm_w [dv] fp32; out [B, T, Hv*dv].
-// The caller advances conv_head by T, as the backend does (:1502).
+// The caller advances conv_head by T, as the backend does (:1506).
 void orc_deltanet_layer(const bf16_t* qkv, int qkv_stride, const bf16_t* z, int z_stride,
                         const bf16_t* a, const bf16_t* b, int ab_stride, const bf16_t* conv_w,
                         float* conv_state, int conv_head, const bf16_t* dt_bias, const float* A_log,

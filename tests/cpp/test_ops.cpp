@@ -26,6 +26,9 @@ void orc_decode_prepare(const uint16_t*, int, uint16_t*, uint16_t*, uint16_t*, c
                         const uint16_t*, uint16_t*, uint16_t*, int, int, int, int, int, int, float, float,
                         const int*);
 void orc_sigmoid_mul(const uint16_t*, const uint16_t*, uint16_t*, long);
+void orc_deltanet_layer(const uint16_t*, int, const uint16_t*, int, const uint16_t*, const uint16_t*, int,
+                        const uint16_t*, float*, int, const uint16_t*, const float*, const float*, float*, uint16_t*,
+                        int, int, int, int, int, int, int, float, float);
 uint16_t orc_f32_to_bf16(float);
 float orc_bf16_to_f32(uint16_t);
 }
@@ -258,6 +261,45 @@ int main() {
       threw = true;
     }
     expect(threw, "apply_rope_partial rejects interleaved mRoPE", 0);
+  }
+  // ---- whole DeltaNet layer: prefill over fused rows, then decode steps ----
+  {
+    const int Hk = 2, Hv = 4, d = 128, K = 4, T0 = 100, steps = 3, T = T0 + steps;
+    const int ch = 2 * Hk * d + Hv * d, zd = Hv * d, all = ch + zd + 2 * Hv;
+    const float eps = 1e-6f;
+    u16v fused = rand_bf16(size_t(T) * all), w = rand_bf16(size_t(ch) * K), dtb = rand_bf16(Hv);
+    std::vector<float> alog(Hv), nw(d), cs0(size_t(K - 1) * ch), S0(size_t(Hv) * d * d);
+    for (auto& x : alog) x = 0.5f * nrand();
+    for (auto& x : nw) x = 1.0f + 0.1f * nrand();
+    for (auto& x : cs0) x = nrand();
+    for (auto& x : S0) x = 0.02f * nrand();
+    Tensor tf = upload(ctx, fused, {T, all}, DType::bf16), tw = upload(ctx, w, {ch, K}, DType::bf16),
+           tdt = upload(ctx, dtb, {Hv}, DType::bf16), tal = upload(ctx, alog, {Hv}, DType::f32),
+           tnw = upload(ctx, nw, {d}, DType::f32), tcs = upload(ctx, cs0, {K - 1, ch}, DType::f32),
+           tst = upload(ctx, S0, {Hv, d, d}, DType::f32);
+    Tensor out = Tensor::allocate(ctx, {T, zd});
+    Tensor ws = Tensor::allocate(ctx, {int64_t(ops::linear_delta_layer_prefill_workspace_bytes(T0, Hk, Hv, d, d))},
+                                 DType::u8);
+    int head = 1;
+    Tensor pre = Tensor::view(ctx, tf.data(), {T0, all});
+    ops::linear_delta_layer_prefill(ctx, pre, out, T0, tw, tcs, head, &tdt, &tal, tnw, tst, ws, Hk, Hv, d, d, K, eps);
+    for (int t = T0; t < T; ++t) {
+      uint16_t* row = tf.data_as<uint16_t>() + size_t(t) * all;
+      Tensor vq = Tensor::view(ctx, row, {1, ch}), vz = Tensor::view(ctx, row + ch, {1, zd}),
+             va = Tensor::view(ctx, row + ch + zd, {1, Hv}), vb = Tensor::view(ctx, row + ch + zd + Hv, {1, Hv}),
+             vo = Tensor::view(ctx, out.data_as<uint16_t>() + size_t(t) * zd, {1, zd});
+      ops::linear_delta_layer_decode(ctx, vq, vz, va, vb, tw, tcs, head, &tdt, &tal, tnw, tst, vo, Hk, Hv, d, d, K,
+                                     eps);
+    }
+    std::vector<float> Sw = S0, csw = cs0;
+    u16v ow(size_t(T) * zd);
+    orc_deltanet_layer(fused.data(), all, fused.data() + ch, all, fused.data() + ch + zd,
+                       fused.data() + ch + zd + Hv, all, w.data(), csw.data(), 1, dtb.data(), alog.data(), nw.data(),
+                       Sw.data(), ow.data(), 1, T, Hk, Hv, d, d, K, eps, 1.0f / std::sqrt(float(d)));
+    const double es = relerr_f(download<float>(ctx, tst), Sw);
+    const double eo = relerr(download<uint16_t>(ctx, out), ow);
+    expect(es <= 1e-3 && eo <= 1e-2 && download<float>(ctx, tcs) == csw && head == (1 + T) % 3,
+           "linear_delta_layer prefill + decode", std::fmax(es, eo));
   }
   std::printf("peak device bytes %zu\n", ctx.peak_allocated_bytes());
   std::printf(g_fail ? "FAILED %d\n" : "ALL OK\n", g_fail);
