@@ -646,9 +646,12 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       sSl[w4][lane] = u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
                             pack_bf16x2(r[6], r[7])};
     };
-    auto chunk = [&](const StateOps& o, int cn, StateOps& on) __attribute__((always_inline)) {
+    // `active` is uniform; an inactive chunk (past the last one, padding the
+    // three-chunk rotation) only issues its loads and barriers.
+    auto chunk = [&](bool active, const StateOps& o, int cn, StateOps& on) __attribute__((always_inline)) {
       // A: D = U - W S (hi*hi + hi*lo + lo*hi), published as bf16 and as
       //    hi/lo bf16 of fk D
+      if (active) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < DK / 32; ++ks) {
@@ -673,9 +676,11 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
         sDh[s2][half][lane] = hp;
         sDl[s2][half][lane] = u32x2{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3])};
       }
+      }
       load(cn, on);
-      __syncthreads();
+      phase_barrier();
       // B: S = gamma S + K^T (fk D) for the key rows of this wave
+      if (active) {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         f32x4 a2 = {0.f, 0.f, 0.f, 0.f};
@@ -691,7 +696,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
         for (int j = 0; j < 4; ++j) s_reg[tt][j] = o.gam * s_reg[tt][j] + a2[j];
       }
       publish_state();
-      __syncthreads();
+      }
+      phase_barrier();
     };
     publish_state();
     // Three operand sets rotate; loads are unconditional (clamped to the
@@ -701,11 +707,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     load(min(1, nch - 1), o1);
     __syncthreads();
     for (int c = 0; c < nch; c += 3) {
-      chunk(o0, min(c + 2, nch - 1), o2);
-      if (c + 1 >= nch) break;
-      chunk(o1, min(c + 3, nch - 1), o0);
-      if (c + 2 >= nch) break;
-      chunk(o2, min(c + 4, nch - 1), o1);
+      chunk(true, o0, min(c + 2, nch - 1), o2);
+      chunk(c + 1 < nch, o1, min(c + 3, nch - 1), o0);
+      chunk(c + 2 < nch, o2, min(c + 4, nch - 1), o1);
     }
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
@@ -723,43 +727,43 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       o.p[1] = P[64];
       o.fq = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(rec + R::kF) + w4 * 16 + g4 * 4);
     };
-    auto chunk = [&](int c, const OutOps& o, int cn, OutOps& on) __attribute__((always_inline)) {
-      const int t0 = c * kC;
-      const int n = min(kC, T - t0);
+    // Output rows go out through a buffer resource bounded at the chunk's
+    // last token, so the stores need no per-row branch (rows past T drop).
+    const int rs2 = Hv * DV * 2;   // bytes per token row
+    const int lane_off = ((w4 * 16 + g4 * 4) * Hv + hv) * DV * 2 + col * 2;
+    auto chunk = [&](bool active, int c, const OutOps& o, int cn, OutOps& on) __attribute__((always_inline)) {
       // A: Q S with the state of this chunk
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (active) {
 #pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sS[ks][lane]), acc);
+        for (int ks = 0; ks < DK / 32; ++ks) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sS[ks][lane]), acc);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] *= o.fq[j];
+        for (int j = 0; j < 4; ++j) acc[j] *= o.fq[j];
+      }
       load(cn, on);
-      __syncthreads();
+      phase_barrier();
       // B: + P D, store
+      if (active) {
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-        if (s2 <= (w4 >> 1)) acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), acc);
-      bf16* orow = out + ((static_cast<size_t>(b) * T + t0 + w4 * 16 + g4 * 4) * Hv + hv) * DV + col;
-      const size_t rs = static_cast<size_t>(Hv) * DV;
-      if (n == kC) {   // full chunk: no per-row guard
-#pragma unroll
-        for (int j = 0; j < 4; ++j) orow[j * rs] = f2bf(scale * acc[j]);
-      } else {
+        for (int s2 = 0; s2 < 2; ++s2)
+          if (s2 <= (w4 >> 1)) acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), acc);
+        const int t0 = c * kC;
+        const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+            out + (static_cast<size_t>(b) * T + t0) * Hv * DV, 0, min(kC, T - t0) * rs2, kBufferRsrcWord3);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (w4 * 16 + g4 * 4 + j < n) orow[j * rs] = f2bf(scale * acc[j]);
+          __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * acc[j]), orsrc, lane_off + j * rs2, 0, 0);
       }
-      __syncthreads();
+      phase_barrier();
     };
     OutOps o0, o1, o2;
     load(0, o0);
     load(min(1, nch - 1), o1);
     __syncthreads();
     for (int c = 0; c < nch; c += 3) {
-      chunk(c, o0, min(c + 2, nch - 1), o2);
-      if (c + 1 >= nch) break;
-      chunk(c + 1, o1, min(c + 3, nch - 1), o0);
-      if (c + 2 >= nch) break;
-      chunk(c + 2, o2, min(c + 4, nch - 1), o1);
+      chunk(true, c, o0, min(c + 2, nch - 1), o2);
+      chunk(c + 1 < nch, c + 1, o1, min(c + 3, nch - 1), o0);
+      chunk(c + 2 < nch, c + 2, o2, min(c + 4, nch - 1), o1);
     }
   }
 }

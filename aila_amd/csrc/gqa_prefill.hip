@@ -115,6 +115,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   __shared__ __attribute__((aligned(1024))) unsigned char sK1[2][C::TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char sV0[2][C::TILE];
   __shared__ __attribute__((aligned(1024))) unsigned char sV1[2][C::TILE];
+  // Group A's second (heavy) query block, staged by DMA in the prologue so
+  // that switching blocks mid-loop costs LDS reads, not a memory round trip.
+  __shared__ __attribute__((aligned(1024))) unsigned char sQh[kWaves * C::QT * C::KS * 1024];
 
   const int grp = __builtin_amdgcn_readfirstlane(threadIdx.x / kThreads);   // 0 = A, 1 = B
   const int t = threadIdx.x % kThreads, lane = t & 63;
@@ -183,6 +186,31 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
       const bf16* qr = q + static_cast<size_t>(row) * q_row_stride + h * D + g4 * 8;
 #pragma unroll
       for (int ks = 0; ks < C::KS; ++ks) qb_op[qt][ks] = as_bf16x8(ld16(qr + ks * 32));
+      m_run[qt] = -INFINITY;
+      l_run[qt] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) o_acc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // The heavy block's Q operands of this wave, in [qt][ks][lane] order.
+  unsigned char* my_qh = sQh + wave * (C::QT * C::KS * 1024);
+  auto stage_segment_q = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int qt = 0; qt < C::QT; ++qt) {
+      const int row = min(qb * C::BM + wave * RPW + qt * 16 + m16, S - 1);
+      const u32x4 src = buffer_rsrc(q + h * D, (S - 1) * q_row_stride * 2 + D * 2);
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks)
+        dma16_to_lds(src, (row * q_row_stride + g4 * 8 + ks * 32) * 2, my_qh + (qt * C::KS + ks) * 1024);
+    }
+  };
+  auto begin_staged_segment = [&](int qb) __attribute__((always_inline)) {
+    seg_qb = qb;
+#pragma unroll
+    for (int qt = 0; qt < C::QT; ++qt) {
+#pragma unroll
+      for (int ks = 0; ks < C::KS; ++ks)
+        qb_op[qt][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(my_qh + (qt * C::KS + ks) * 1024 + lane * 16));
       m_run[qt] = -INFINITY;
       l_run[qt] = 0.f;
 #pragma unroll
@@ -352,12 +380,35 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     }
   };
 
-  // ---- prologue: K_0, V_0, K_1 -------------------------------------------
+  // ---- fused copy_to_cache: this pair's own K/V rows, shared by the G query
+  //      heads of the KV group (head h copies every G-th row from h % G).
+  auto copy_rows_to_cache = [&]() __attribute__((always_inline)) {
+    if (k_cache != nullptr) {
+      const int gi = h % G;
+#pragma unroll 1
+      for (int pass = 0; pass < 2; ++pass) {
+        const int qb = pass == 0 ? qh : ql;
+        if (pass == 1 && ql == qh) break;
+        const int r0 = qb * C::BM, r1 = min(r0 + C::BM, S);
+        const int nrow = (r1 - r0 - gi + G - 1) / G;   // rows r0 + gi, r0 + gi + G, ...
+        for (int p = threadIdx.x; p < nrow * C::NC; p += 2 * kThreads) {
+          const int row = r0 + gi + (p / C::NC) * G, c = p % C::NC;
+          const size_t src = static_cast<size_t>(row) * kv_row_stride + c * 8;
+          const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + row) * D + c * 8;
+          *reinterpret_cast<u32x4*>(k_cache + dst) = ld16(Kh + src);
+          *reinterpret_cast<u32x4*>(v_cache + dst) = ld16(Vh + src);
+        }
+      }
+    }
+  };
+
+  // ---- prologue: K_0, V_0, K_1 (+ group A's heavy Q) ------------------------
   if (my_n > 0) {
     begin_segment(qb_of(0));
     issue_tile(sK0[grp], Kh, koff, kb_of(0));
     issue_tile(sV0[grp], Vh, voff, kb_of(0));
     if (my_n > 1) issue_tile(sK1[grp], Kh, koff, kb_of(1));
+    if (grp == 0 && nl > 0 && hsplit > 0) stage_segment_q(qh);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   __syncthreads();
@@ -375,8 +426,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     if (j < my_n) {
       if (j >= 1 && qb_of(j) != qb_of(j - 1)) {   // group A moves from its light to its heavy block
         store_segment();
-        begin_segment(qb_of(j));
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+        begin_staged_segment(qb_of(j));             // staged in the prologue, long complete
       }
       s_block(kcur, kb_of(j));
     } else {
@@ -463,23 +513,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   } else if (b_has_heavy && grp == 1) {
     store_segment();
   }
-
-  // ---- fused copy_to_cache: this pair's own K/V rows, one head per KV group --
-  if (k_cache != nullptr && h % G == 0) {
-#pragma unroll 1
-    for (int pass = 0; pass < 2; ++pass) {
-      const int qb = pass == 0 ? qh : ql;
-      if (pass == 1 && ql == qh) break;
-      const int r0 = qb * C::BM, r1 = min(r0 + C::BM, S);
-      for (int p = threadIdx.x; p < (r1 - r0) * C::NC; p += 2 * kThreads) {
-        const int row = r0 + p / C::NC, c = p % C::NC;
-        const size_t src = static_cast<size_t>(row) * kv_row_stride + c * 8;
-        const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + row) * D + c * 8;
-        *reinterpret_cast<u32x4*>(k_cache + dst) = ld16(Kh + src);
-        *reinterpret_cast<u32x4*>(v_cache + dst) = ld16(Vh + src);
-      }
-    }
-  }
+  copy_rows_to_cache();
 }
 
 template <int D, int RPW, int BN>
