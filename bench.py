@@ -410,6 +410,38 @@ def sub_decode_prep(torch, aila_amd, per_graph=32, reps=20):
             "us_per_call": round(us, 2), "GBps": round(byts / us / 1e3, 1)}
 
 
+def sub_deltanet_layer_prefill(torch, aila_amd, reps=10):
+    """Full layer prefill (conv ring + SiLU into hi/lo planes, chunked
+    recurrence with the key/value residuals, RMSNorm*SiLU(z) gate) at the
+    config-4 shape, from the backend's fused [qkv | z | a | b] rows."""
+    B, T, Hk, Hv, d = 1, 4096, 16, 32, 128
+    ch, zd = 2 * Hk * d + Hv * d, Hv * d
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 7)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    fused = torch.randn((B, T, ch + zd + 2 * Hv), generator=g, **bf)
+    w = torch.randn((ch, 4), generator=g, **bf) * 0.5
+    cs = torch.zeros((B, 3, ch), dtype=torch.float32, device="cuda")
+    nw = torch.ones(d, dtype=torch.float32, device="cuda")
+    st = torch.zeros((B, Hv, d, d), dtype=torch.float32, device="cuda")
+    ws = torch.empty(aila_amd.deltanet_layer_prefill_workspace_size(B, T, Hk, Hv), dtype=torch.uint8, device="cuda")
+    out = torch.empty((B, T, zd), **bf)
+    fn = lambda: aila_amd.deltanet_layer_prefill(fused[..., :ch], fused[..., ch:ch + zd],
+                                                 fused[..., ch + zd:ch + zd + Hv], fused[..., ch + zd + Hv:], w, cs, 0,
+                                                 nw, st, Hk, out=out, workspace=ws)
+    fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    us = s.elapsed_time(e) / reps * 1e3
+    return {"config": f"layer prefill T={T} Hk={Hk} Hv={Hv} d={d} (fused rows)", "us": round(us, 1),
+            "tok_per_s": round(T / (us * 1e-6))}
+
+
 def sub_decode_cfg1(torch, aila_amd, per_graph=32, reps=20):
     B, Hq, Hkv, D, L = 1, 16, 8, 128, 512
     g = torch.Generator(device="cuda")
@@ -491,7 +523,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
                     choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill",
-                             "deltanet_layer_decode", "decode_prep"],
+                             "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     args = ap.parse_args()
@@ -510,6 +542,7 @@ def main():
          "deltanet_decode": lambda t, a: sub_deltanet_decode(t, a, steps=320),
          "deltanet_prefill": lambda t, a: sub_deltanet_prefill(t, a, reps=20),
          "deltanet_layer_decode": lambda t, a: sub_deltanet_layer_decode(t, a, steps=320),
+         "deltanet_layer_prefill": lambda t, a: sub_deltanet_layer_prefill(t, a, reps=10),
          "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20)}[args.profile_kernel](torch, aila_amd)
         if r:
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
@@ -531,6 +564,8 @@ def main():
         sub["deltanet_layer_decode"] = sub_deltanet_layer_decode(torch, aila_amd)
         log(f"[bench] deltanet layer decode {sub['deltanet_layer_decode']}")
         sub["deltanet_prefill"] = sub_deltanet_prefill(torch, aila_amd)
+        sub["deltanet_layer_prefill"] = sub_deltanet_layer_prefill(torch, aila_amd)
+        log(f"[bench] deltanet layer prefill {sub['deltanet_layer_prefill']}")
         log(f"[bench] deltanet prefill {sub['deltanet_prefill']}")
         sub["gqa_decode_cfg1"] = sub_decode_cfg1(torch, aila_amd)
         sub["decode_prep"] = sub_decode_prep(torch, aila_amd)
