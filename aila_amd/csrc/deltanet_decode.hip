@@ -7,28 +7,32 @@
 // state column slab lives in VGPRs between the two reductions.
 //
 // Work decomposition: one 256-thread workgroup per (value head, sequence,
-// 128-column slab of dv). Thread t owns columns 4*(t%32)..+3 of the slab and
-// rows (t/32)*RPT..+RPT-1 of dk (RPT = dk/8). Loads are float4 along dv, so a
-// wave reads two 512-byte row segments per instruction. The column sums
-// u = S^T k and o = S^T q are reduced over the 8 row groups with one
-// lane-swap (row groups 2w and 2w+1 share wave w) and an LDS pass over the 4
-// waves.
+// slab of 4*CQ columns of dv), CQ = 32 or 16. Thread t owns columns
+// 4*(t%CQ)..+3 of the slab and rows (t/CQ)*RPT..+RPT-1 of dk (RPT = dk /
+// (256/CQ)). Loads are float4 along dv, so a wave reads 512- or 256-byte row
+// segments per instruction. The column sums u = S^T k and o = S^T q are
+// reduced over the row groups of a wave with lane swaps and over the 4
+// waves through LDS. The narrower slab (CQ = 16) doubles the workgroups for
+// small batches, where one workgroup per CU leaves the state load latency
+// exposed (config-5 DeltaNet layer, B = 8: 7.2 -> see the launcher).
 #include "common.hpp"
+
+#include <type_traits>
 
 namespace aila {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kColQuads = 32;   // 128 columns per workgroup
-constexpr int kRowGroups = 8;
 
-template <int DK>
+template <int DK, int CQ>
 __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, const bf16* __restrict__ a,
     const bf16* __restrict__ bgate, const bf16* __restrict__ dt_bias,
     const float* __restrict__ A_log, float* __restrict__ state,
     bf16* __restrict__ out, int Hk, int Hv, int dv, float eps, float scale) {
+  constexpr int kColQuads = CQ;
+  constexpr int kRowGroups = kThreads / CQ;
   constexpr int RPT = DK / kRowGroups;  // rows per thread
   const int hv = blockIdx.x;
   const int bseq = blockIdx.y;
@@ -110,10 +114,12 @@ __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
     s[r] *= decay;
     u += s[r] * kr[r];
   }
-  // Row groups 2w and 2w+1 live in lanes [0,32) and [32,64) of wave w.
+  // The 64 / CQ row groups of wave w live in lane blocks of CQ.
 #pragma unroll
-  for (int e = 0; e < 4; ++e) u[e] += __shfl_xor(u[e], 32);
-  if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[0][wave][cq * 4]) = u;
+  for (int m = CQ; m < 64; m <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) u[e] += __shfl_xor(u[e], m);
+  if (lane < CQ) *reinterpret_cast<f32x4*>(&s_red[0][wave][cq * 4]) = u;
   __syncthreads();
   u = *reinterpret_cast<const f32x4*>(&s_red[0][0][cq * 4]) +
       *reinterpret_cast<const f32x4*>(&s_red[0][1][cq * 4]) +
@@ -143,8 +149,10 @@ __global__ __launch_bounds__(kThreads) void deltanet_decode_kernel(
     }
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], 32);
-  if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[1][wave][cq * 4]) = o;
+  for (int m = CQ; m < 64; m <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], m);
+  if (lane < CQ) *reinterpret_cast<f32x4*>(&s_red[1][wave][cq * 4]) = o;
   __syncthreads();
   if (t < kColQuads && active) {
     o = *reinterpret_cast<const f32x4*>(&s_red[1][0][cq * 4]) +
@@ -175,7 +183,6 @@ extern "C" int aila_hip_deltanet_decode(const void* q, const void* k,
                "deltanet_decode: need B, Hk, Hv > 0 and Hv %% Hk == 0 (B=%d Hk=%d Hv=%d)", B, Hk, Hv);
   AILA_REQUIRE(dv > 0 && dv % 4 == 0, "deltanet_decode: dv must be a positive multiple of 4 (dv=%d)", dv);
   AILA_REQUIRE(B <= 65535, "deltanet_decode: B too large (%d)", B);
-  const dim3 grid(Hv, B, (dv + kColQuads * 4 - 1) / (kColQuads * 4));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bf16* qp = static_cast<const bf16*>(q);
   const bf16* kp = static_cast<const bf16*>(k);
@@ -184,19 +191,22 @@ extern "C" int aila_hip_deltanet_decode(const void* q, const void* k,
   const bf16* bp = static_cast<const bf16*>(b);
   const bf16* dtp = static_cast<const bf16*>(dt_bias);
   bf16* op = static_cast<bf16*>(out);
+  // 128-column slabs unless that leaves fewer than two workgroups per CU.
+  const bool narrow = static_cast<long>(B) * Hv * ((dv + 127) / 128) < 512;
+  auto launch = [&](auto dk_tag, auto cq_tag) {
+    constexpr int DK = decltype(dk_tag)::value, CQ = decltype(cq_tag)::value;
+    const dim3 grid(Hv, B, (dv + CQ * 4 - 1) / (CQ * 4));
+    hipLaunchKernelGGL((deltanet_decode_kernel<DK, CQ>), grid, dim3(kThreads), 0, st, qp, kp, vp, ap, bp, dtp,
+                       A_log, state, op, Hk, Hv, dv, eps, scale);
+  };
+  auto with_cq = [&](auto dk_tag) {
+    if (narrow) launch(dk_tag, std::integral_constant<int, 16>{});
+    else launch(dk_tag, std::integral_constant<int, 32>{});
+  };
   switch (dk) {
-    case 64:
-      hipLaunchKernelGGL(deltanet_decode_kernel<64>, grid, dim3(kThreads), 0, st, qp, kp, vp, ap,
-                         bp, dtp, A_log, state, op, Hk, Hv, dv, eps, scale);
-      break;
-    case 128:
-      hipLaunchKernelGGL(deltanet_decode_kernel<128>, grid, dim3(kThreads), 0, st, qp, kp, vp, ap,
-                         bp, dtp, A_log, state, op, Hk, Hv, dv, eps, scale);
-      break;
-    case 256:
-      hipLaunchKernelGGL(deltanet_decode_kernel<256>, grid, dim3(kThreads), 0, st, qp, kp, vp, ap,
-                         bp, dtp, A_log, state, op, Hk, Hv, dv, eps, scale);
-      break;
+    case 64: with_cq(std::integral_constant<int, 64>{}); break;
+    case 128: with_cq(std::integral_constant<int, 128>{}); break;
+    case 256: with_cq(std::integral_constant<int, 256>{}); break;
     default:
       return set_error(AILA_HIP_EUNSUPPORTED, "deltanet_decode: dk=%d not in {64,128,256}", dk);
   }
