@@ -256,6 +256,11 @@ def sub_prefill(torch, aila_amd, reps=20):
     q = torch.randn((S, Hq * D), generator=g, **bf)
     k = torch.randn((S, Hkv * D), generator=g, **bf)
     v = torch.randn((S, Hkv * D), generator=g, **bf)
+    # config 2's inputs: per-head QK RMS-norm (weight 1) and NeoX RoPE
+    # (theta 1e6, positions 0..S-1) on q and k, prepared outside the timing
+    aila_amd.head_rms_norm(q.view(S, Hq, D), eps=1e-6)
+    aila_amd.head_rms_norm(k.view(S, Hkv, D), eps=1e-6)
+    aila_amd.apply_rope(q.view(S, Hq, D), k.view(S, Hkv, D), start_pos=0, rotary_dim=D, theta=1e6)
     out = torch.empty_like(q)
     kc = torch.empty((Hkv, S, D), **bf)
     vc = torch.empty_like(kc)
@@ -271,7 +276,7 @@ def sub_prefill(torch, aila_amd, reps=20):
     torch.cuda.synchronize()
     us = s.elapsed_time(e) / reps * 1e3
     flops = 4 * D * Hq * S * (S + 1) / 2
-    return {"config": "2: S=2048 Hq=32 Hkv=8 D=128 causal + cache write", "us": round(us, 2),
+    return {"config": "2: S=2048 Hq=32 Hkv=8 D=128 causal (QK-normed, RoPE'd inputs) + cache write", "us": round(us, 2),
             "tflops": round(flops / us / 1e6, 1), "frac_of_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
 
 
