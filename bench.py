@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention hot path (one GPU).
 
-Headline workload: decode of a Qwen3.5-4B-shaped hybrid
+Headline workload (benchmark config 5): decode of a Qwen3.5-4B-shaped hybrid
 attention stack, 32 layers in a 3:1 pattern (24 Gated DeltaNet layers with
 16 qk / 32 v heads, dk = dv = 128, fp32 state; 8 GQA layers with 16 q / 4 kv
 heads, head_dim 256, bf16 KV cache), batch 8, context 32768, one new token

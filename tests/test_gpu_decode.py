@@ -64,7 +64,7 @@ def _decode_case(seed, B, Hq, Hkv, D, max_seq, L, split=True, seq_lens=None, poi
 
 @pytest.mark.parametrize("split", [True, False])
 def test_decode_config1_qwen3_0p6b(split):
-    # B=1, 16 q heads, 8 kv heads, D=128, context 512.
+    # benchmark config 1: B=1, 16 q heads, 8 kv heads, D=128, context 512.
     _decode_case(0xA11A, 1, 16, 8, 128, 520, 512, split=split)
 
 
@@ -89,7 +89,7 @@ def test_decode_zero_length():
 
 
 def test_decode_long_context_qwen35_shape():
-    # One layer of BASELINE config 5 at reduced batch: 16q/4kv, D=256, 32k.
+    # One layer of benchmark config 5 at reduced batch: 16q/4kv, D=256, 32k.
     _decode_case(3004, 1, 16, 4, 256, 32768 + 8, 32768, split=True, poison=True)
 
 
@@ -158,7 +158,7 @@ def test_deltanet_decode_short(Hk, Hv, dk, dv):
 
 
 def test_deltanet_decode_2048_steps_state_tolerance():
-    # BASELINE config 3 statistics (N(0,0.02) state, L2-normed q/k, sigmoid
+    # benchmark config 3 statistics (N(0,0.02) state, L2-normed q/k, sigmoid
     # beta, alpha = exp(-softplus(a))) with B=4, H=16 to keep the oracle fast.
     B, T, H, d = 4, 2048, 16, 128
     q, k, v, a, b, S0 = _dn_inputs(0xA11A + 2, B, T, H, H, d, d)

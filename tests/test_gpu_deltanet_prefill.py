@@ -61,7 +61,7 @@ def _case(seed, B, T, Hk, Hv, d=128, s0_std=0.02, gates=False):
 
 
 def test_prefill_config4_qwen35():
-    # T=4096, chunk 64, 16 q/k heads, 32 v heads, zero state.
+    # benchmark config 4: T=4096, chunk 64, 16 q/k heads, 32 v heads, zero state.
     _case(0xA11A + 3, 1, 4096, 16, 32, s0_std=0.0)
 
 

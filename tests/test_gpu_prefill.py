@@ -31,7 +31,7 @@ def _relerr(a, r):
 
 
 def qk_prepped(seed, S, Hq, Hkv, D, start_pos=0, theta=1e6):
-    """BASELINE config-2 inputs: N(0,1) bf16, QK RMS-norm, RoPE, bf16 after each."""
+    """Benchmark config-2 inputs: N(0,1) bf16, QK RMS-norm, RoPE, bf16 after each."""
     q = dg.normal_bf16(seed, 0, (S, Hq * D))
     k = dg.normal_bf16(seed, 1, (S, Hkv * D))
     v = dg.normal_bf16(seed, 2, (S, Hkv * D))
@@ -78,7 +78,7 @@ def _prefill_case(seed, S, Hq, Hkv, D, with_cache=False, cache_pos=0, prepped=Fa
 
 
 def test_prefill_config2_qwen3_4b():
-    # S=2048, 32 q heads, 8 kv heads, D=128, QK-norm, RoPE 1e6,
+    # benchmark config 2: S=2048, 32 q heads, 8 kv heads, D=128, QK-norm, RoPE 1e6,
     # causal; the KV cache is written for later decode.
     _prefill_case(0xA11A + 1, 2048, 32, 8, 128, with_cache=True, prepped=True)
 
