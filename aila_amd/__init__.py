@@ -28,6 +28,8 @@ _SIGS = {
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_gqa_decode_prepare_append": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I,
+                                            _I, _F, _F, _I, _P, _P], _I),
     "aila_hip_kv_append": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_prefill": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_gqa_prefill_cached": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -474,6 +476,44 @@ def decode_prepare_qkv(q_in, k, v, q_norm_w=None, k_norm_w=None, k_cache=None, v
         _ptr(positions), _stream(stream))
     _check(rc, "decode_prepare_qkv")
     return (q_out, gate_out) if packed_gate else q_out
+
+
+def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_norm_w=None, k_norm_w=None,
+                              rotary_dim=None, theta: float = 1e6, eps: float = 1e-6, packed_gate: bool = False,
+                              out=None, gate_out=None, workspace=None, positions=None, stream=None):
+    """QK-norm + RoPE + K/V append + split-K decode in one launch.
+    q_in [B,Hq,D] (or [B,Hq,2D] q|gate when packed_gate); k_new/v_new [B,Hkv,D];
+    caches [B,Hkv,max_seq,D]. Returns out (and gate_out when packed)."""
+    import torch
+    B, Hkv, max_seq, D = k_cache.shape
+    Hq = q_in.shape[1]
+    _need(q_in, torch.bfloat16, (B, Hq, 2 * D if packed_gate else D), "q_in")
+    _need(k_new, torch.bfloat16, (B, Hkv, D), "k_new")
+    _need(v_new, torch.bfloat16, (B, Hkv, D), "v_new")
+    _need(k_cache, torch.bfloat16, (B, Hkv, max_seq, D), "k_cache")
+    _need(v_cache, torch.bfloat16, (B, Hkv, max_seq, D), "v_cache")
+    for w, name in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        if w is not None:
+            _need(w, torch.bfloat16, (D,), name, align=2)
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k_cache.device)
+    _need(out, torch.bfloat16, (B, Hq, D), "out")
+    if packed_gate:
+        if gate_out is None:
+            gate_out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k_cache.device)
+        _need(gate_out, torch.bfloat16, (B, Hq, D), "gate_out")
+    if workspace is None:
+        workspace = torch.empty(gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device=k_cache.device)
+    if positions is not None:
+        _need(positions, torch.int32, (B,), "positions", align=4)
+    rc = lib().aila_hip_gqa_decode_prepare_append(
+        _ptr(q_in), int(bool(packed_gate)), _ptr(gate_out) if packed_gate else None, _ptr(k_new), _ptr(v_new),
+        _ptr(q_norm_w), _ptr(k_norm_w), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(workspace),
+        workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, max_seq,
+        D if rotary_dim is None else int(rotary_dim), float(theta), float(eps), int(pos), _ptr(positions),
+        _stream(stream))
+    _check(rc, "gqa_decode_prepare_append")
+    return (out, gate_out) if packed_gate else out
 
 
 def head_rms_norm(x, weight=None, eps: float = 1e-6, stream=None):

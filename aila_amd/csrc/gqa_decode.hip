@@ -48,13 +48,27 @@ __device__ __forceinline__ int kswz(int r) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int D, int G>
+// Fused decode preparation (decode_prepare_qkv[_partial] / qgkv_packed,
+// ElementwiseOps.cpp:105-216, 555-863) applied inside the decode: q and the
+// new k get per-head RMSNorm (rounded to bf16), then NeoX RoPE over the
+// first `rot` dims at the token's position (rounded to bf16); the gate half
+// of a packed q|gate head is copied to gate_out by split 0.
+struct PrepArgs {
+  int q_stride;          // elements between query heads of q_in (D, or 2D packed)
+  const bf16* qn_w;      // [D] or null
+  const bf16* kn_w;      // [D] or null
+  bf16* gate_out;        // [B, Hq, D] (packed only) or null
+  int rot;               // rotary dims, even, in [2, D]
+  float theta, eps;
+};
+
+template <int D, int G, bool PREP = false>
 __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kc,
     const bf16* __restrict__ vc, bf16* __restrict__ out,
     float* __restrict__ part, int Hq, int Hkv, int max_seq, int L,
     const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max,
-    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new) {
+    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new, PrepArgs pa) {
   static_assert(D % 32 == 0 && D <= 256, "D");
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "G");
   constexpr int KS = D / 32;          // MFMA k-steps over the head dim
@@ -84,29 +98,11 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   __shared__ __attribute__((aligned(1024))) unsigned char s_k[kWaves][2][STAGE];
   __shared__ float s_p[kWaves][kChunk][G];
   __shared__ float s_ml[kWaves][2][G];
+  __shared__ float s_q[PREP ? G : 1][PREP ? D : 1];   // prepared q (fused preparation only)
+  __shared__ float s_tab[PREP ? D : 1];               // (cos, sin) per rotary pair
   static_assert(sizeof(float) * kWaves * G * D <= sizeof(s_k), "epilogue reuses the K ring");
   // epilogue: per-wave accumulators, in the (then idle) K ring
   float (*s_acc)[G][D] = reinterpret_cast<float (*)[G][D]>(&s_k[0][0][0]);
-
-  // Query operand (A rows = heads, zero rows for m16 >= G).
-  bf16x8_t qa[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (m16 < G) raw = ld16(q + (static_cast<size_t>(b) * Hq + h0 + m16) * D + ks * 32 + g4 * 8);
-    qa[ks] = as_bf16x8(raw);
-  }
-
-  float m_run[G], l_part[G], acc[G][8];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m_run[h] = -INFINITY;
-    l_part[h] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-  }
-  const int vd = (lane % VL) * 8;
-  const int vr = lane / VL;
 
   // K rows of one 16-token chunk -> this wave's LDS stage, whole rows per
   // DMA instruction (lane order within a row follows the swizzle).
@@ -122,9 +118,135 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     }
   };
 
+  // The first chunk's K DMA goes out before the query work whenever that
+  // chunk cannot hold the row this launch appends (fused preparation).
+  int t0 = s0 + wave * kChunk;
+  const bool early = PREP && t0 < s1 && t0 + kChunk <= len - 1;
+  if (early) dma_k(0, t0);
+
+  // Query operand (A rows = heads, zero rows for m16 >= G).
+  bf16x8_t qa[KS];
+  if constexpr (!PREP) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (m16 < G) raw = ld16(q + (static_cast<size_t>(b) * Hq + h0 + m16) * D + ks * 32 + g4 * 8);
+      qa[ks] = as_bf16x8(raw);
+    }
+  } else {
+    // Prepared q, computed once per workgroup: wave w normalises heads w and
+    // w + 4 (one wave per head, D/64 dims per lane), the RoPE pass rotates
+    // pairs in place, and every wave then reads its A operands from LDS.
+    const int p = len - 1, half = pa.rot / 2;
+    for (int j = threadIdx.x; j < half; j += kThreads) {
+      const float freq = 1.0f / powf(pa.theta, (2.0f * j) / static_cast<float>(pa.rot));
+      const float ang = static_cast<float>(p) * freq;
+      s_tab[2 * j] = cosf(ang);
+      s_tab[2 * j + 1] = sinf(ang);
+    }
+    constexpr int E = D / 64;
+#pragma unroll
+    for (int hh = wave; hh < G; hh += kWaves) {
+      const bf16* qr = q + (static_cast<size_t>(b) * Hq + h0 + hh) * pa.q_stride;
+      float xv[E], ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        xv[i] = bf2f(qr[lane + 64 * i]);
+        ss = fmaf(xv[i], xv[i], ss);
+      }
+      ss = wave_sum(ss);
+      const float rms = sqrtf(ss / static_cast<float>(D) + pa.eps);
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int d = lane + 64 * i;
+        const float w = pa.qn_w ? bf2f(pa.qn_w[d]) : 1.0f;
+        s_q[hh][d] = bf2f(f2bf((xv[i] / rms) * w));
+      }
+      // packed q|gate: split 0 copies the gate half through
+      if (pa.gate_out != nullptr && split == 0)
+        for (int d = lane; d < D; d += 64)
+          pa.gate_out[(static_cast<size_t>(b) * Hq + h0 + hh) * D + d] = qr[D + d];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * half; idx += kThreads) {
+      const int hh = idx / half, j = idx % half;
+      const float x0 = s_q[hh][j], x1 = s_q[hh][j + half];
+      const float c = s_tab[2 * j], sn = s_tab[2 * j + 1];
+      s_q[hh][j] = bf2f(f2bf(x0 * c - x1 * sn));
+      s_q[hh][j + half] = bf2f(f2bf(x1 * c + x0 * sn));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (m16 < G) {
+        const float* r = &s_q[m16][ks * 32 + g4 * 8];
+        w = u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
+                  pack_bf16x2(r[6], r[7])};
+      }
+      qa[ks] = as_bf16x8(w);
+    }
+  }
+
+  float m_run[G], l_part[G], acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m_run[h] = -INFINITY;
+    l_part[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  }
+  const int vd = (lane % VL) * 8;
+  const int vr = lane / VL;
+
   // Fused append (decode_prepare's cache write): the workgroup owning the
   // last row writes the new token's K and V there before anything reads it.
-  if (k_new != nullptr && len > 0 && split == nsplit_b - 1) {
+  if (PREP && len > 0 && split == nsplit_b - 1) {
+    // the new k row: RMSNorm + RoPE at row len-1, staged through wave 0's
+    // second K stage (untouched until the loop), then k and v rows written
+    if (wave == 0) {
+      float* sx = reinterpret_cast<float*>(&s_k[0][1][0]);
+      static_assert(STAGE >= D * sizeof(float), "k staging fits");
+      const bf16* kr = k_new + (static_cast<size_t>(b) * Hkv + kvh) * D;
+      constexpr int E = D / 64;
+      float xv[E], ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        xv[i] = bf2f(kr[lane + 64 * i]);
+        ss = fmaf(xv[i], xv[i], ss);
+      }
+      ss = wave_sum(ss);
+      const float rms = sqrtf(ss / static_cast<float>(D) + pa.eps);
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int d = lane + 64 * i;
+        const float w = pa.kn_w ? bf2f(pa.kn_w[d]) : 1.0f;
+        sx[d] = bf2f(f2bf((xv[i] / rms) * w));
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int p = len - 1, half = pa.rot / 2;
+      const float* tab = s_tab;
+      bf16* krow = const_cast<bf16*>(K) + static_cast<size_t>(p) * D;
+      bf16* vrow = const_cast<bf16*>(V) + static_cast<size_t>(p) * D;
+      const bf16* vsrc = v_new + (static_cast<size_t>(b) * Hkv + kvh) * D;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int d = lane + 64 * i;
+        float r = sx[d];
+        if (d < pa.rot) {
+          const int dd = d < half ? d : d - half;
+          const float c = tab[2 * dd], sn = tab[2 * dd + 1];
+          r = d < half ? sx[d] * c - sx[d + half] * sn : sx[d] * c + sx[d - half] * sn;
+        }
+        krow[d] = f2bf(r);
+        vrow[d] = vsrc[d];
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+    }
+    __syncthreads();
+  } else if (k_new != nullptr && len > 0 && split == nsplit_b - 1) {
     if (wave == 0 && lane < 2 * NC) {
       const int row = len - 1;
       const bool isv = lane >= NC;
@@ -137,8 +259,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     __syncthreads();
   }
 
-  int t0 = s0 + wave * kChunk;
-  if (t0 < s1) dma_k(0, t0);
+  if (!early && t0 < s1) dma_k(0, t0);
   for (int it = 0; t0 < s1; ++it, t0 += kWaves * kChunk) {
     const int stage = it & 1;
     // ---- K operands of this chunk (its DMA was issued one chunk earlier) --
@@ -367,14 +488,20 @@ struct DecodeArgs {
   int split_len, nsplit, nsplit_max;
   const bf16* k_new;     // fused append (null: none)
   const bf16* v_new;
+  PrepArgs prep;         // q_stride = 0: no fused preparation
 };
 
 template <int D, int G>
 int launch_decode(const DecodeArgs& a, hipStream_t st) {
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-  hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
-                     a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                     a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new);
+  if (a.prep.q_stride > 0)
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
+                       a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep);
+  else
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
+                       a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep);
   if (a.part) {
     hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
                        a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit_max);
@@ -436,7 +563,7 @@ int dispatch_g(int G, const DecodeArgs& a, hipStream_t st) {
 int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, void* workspace,
                     size_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_seq, int cached_len,
                     const int* seq_lens, int len_bias, const void* k_new, const void* v_new,
-                    hipStream_t st) {
+                    hipStream_t st, const PrepArgs* prep = nullptr) {
   AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
   AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
                "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
@@ -451,6 +578,7 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
   a.seq_lens = seq_lens; a.len_bias = len_bias;
   a.k_new = static_cast<const bf16*>(k_new);
   a.v_new = static_cast<const bf16*>(v_new);
+  a.prep = prep ? *prep : PrepArgs{};
   // Records per (sequence, head) that the workspace holds; the split count
   // adapts to it (the reference's [Hq, max_tiles, 272] partials buffer for
   // D=256 is accepted as-is).
@@ -509,6 +637,32 @@ extern "C" int aila_hip_gqa_decode_append(const void* q, const void* k_new, cons
   AILA_REQUIRE(pos >= 0 && pos < max_seq, "gqa_decode_append: pos=%d outside [0, max_seq=%d)", pos, max_seq);
   return gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, pos + 1,
                          positions, 1, k_new, v_new, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_gate, void* gate_out,
+                                                  const void* k_new, const void* v_new, const void* q_norm_w,
+                                                  const void* k_norm_w, void* k_cache, void* v_cache, void* out,
+                                                  void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
+                                                  int D, int max_seq, int rotary_dim, float theta, float eps,
+                                                  int pos, const int* positions, void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(k_new && v_new, "gqa_decode_prepare_append: null k_new/v_new");
+  AILA_REQUIRE(!packed_gate || gate_out, "gqa_decode_prepare_append: packed q|gate needs gate_out");
+  AILA_REQUIRE(pos >= 0 && pos < max_seq, "gqa_decode_prepare_append: pos=%d outside [0, max_seq=%d)", pos,
+               max_seq);
+  AILA_REQUIRE(theta > 0.f && eps >= 0.f, "gqa_decode_prepare_append: bad theta/eps");
+  int rot = std::max(2, std::min(D, rotary_dim));
+  if (rot & 1) --rot;
+  PrepArgs pa{};
+  pa.q_stride = packed_gate ? 2 * D : D;
+  pa.qn_w = static_cast<const bf16*>(q_norm_w);
+  pa.kn_w = static_cast<const bf16*>(k_norm_w);
+  pa.gate_out = packed_gate ? static_cast<bf16*>(gate_out) : nullptr;
+  pa.rot = rot;
+  pa.theta = theta;
+  pa.eps = eps;
+  return gqa_decode_impl(q_in, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, pos + 1,
+                         positions, 1, k_new, v_new, static_cast<hipStream_t>(stream), &pa);
 }
 
 namespace aila {

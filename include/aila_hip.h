@@ -81,6 +81,30 @@ int aila_hip_gqa_decode_append(const void* q, const void* k_new,
                                int D, int max_seq, int pos,
                                const int* positions, void* stream);
 
+/* The whole attention decode step of a GQA layer in one split-K launch:
+ * ops::decode_prepare_qkv_partial / decode_prepare_qgkv_packed_partial
+ * (src/ops/ElementwiseOps.cpp:555-863: per-head RMSNorm of q and k rounded to
+ * bf16, NeoX RoPE over the first rotary_dim dims at the token's position
+ * rounded to bf16, K/V append) followed by ops::attention_decode, as the
+ * hybrid backend calls them (Qwen35HybridTextBackend.cpp:2109-2180).
+ *   q_in [B, Hq, D] bf16, or [B, Hq, 2D] q|gate per head when packed_gate
+ *   (the gate half is copied to gate_out [B, Hq, D]); k_new/v_new
+ *   [B, Hkv, D]; q_norm_w/k_norm_w [D] bf16 or NULL (weight 1). The prepared
+ *   k and v_new go to cache row pos (or positions[b]) and sequence b attends
+ *   rows [0, row]; q_in and k_new are not modified (the prepared q lives only
+ *   in LDS). rotary_dim is clamped to [2, D] and made even. Other arguments
+ *   as aila_hip_gqa_decode. */
+int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_gate,
+                                       void* gate_out, const void* k_new,
+                                       const void* v_new, const void* q_norm_w,
+                                       const void* k_norm_w, void* k_cache,
+                                       void* v_cache, void* out,
+                                       void* workspace, size_t workspace_bytes,
+                                       int B, int Hq, int Hkv, int D,
+                                       int max_seq, int rotary_dim, float theta,
+                                       float eps, int pos, const int* positions,
+                                       void* stream);
+
 /* Append one decoded token's K and V per sequence to the cache (the
  * cache-write half of ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:
  * 105-216, without the norm/RoPE): k_new/v_new [B, Hkv, D] bf16 ->

@@ -148,3 +148,58 @@ def test_sigmoid_mul(n):
     torch.cuda.synchronize()
     _agree(_np(out), want)
     assert np.array_equal(_np(out), _np(xd))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,rot,packed,device_pos", [
+    (3, 16, 4, 256, 64, True, True),     # Qwen3.5 attention layer
+    (2, 16, 8, 128, 128, False, False),  # Qwen3
+    (2, 8, 1, 128, 32, True, True),      # narrow rotary, eight heads per group
+])
+def test_fused_prepare_append_decode(B, Hq, Hkv, D, rot, packed, device_pos):
+    """One launch (QK-norm + RoPE + append + split-K decode) against the
+    oracle's prep followed by its attention, and against the two-launch
+    path (decode_prepare_qkv + gqa_decode_append)."""
+    import torch
+    import aila_amd
+    seed, theta, eps, max_seq = 760 + D, 1e7, 1e-6, 2048
+    pos = np.array([5, 700, 2047][:B], np.int32) if device_pos else np.full(B, 1500, np.int32)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D if packed else D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
+    kc_d, vc_d = _t(kc), _t(vc)
+    res = aila_amd.gqa_decode_prepare_append(
+        _t(q), _t(k), _t(v), kc_d, vc_d, int(pos.max()), q_norm_w=_t(qw), k_norm_w=_t(kw), rotary_dim=rot,
+        theta=theta, eps=eps, packed_gate=packed, positions=_t(pos) if device_pos else None)
+    torch.cuda.synchronize()
+    out, gate = res if packed else (res, None)
+    # oracle: prep, append, attention per sequence
+    qo, gw, ko = oracle.decode_prepare(q, k, v, qw, kw, kc, vc, pos, B, Hq, Hkv, D, max_seq, rot, theta, eps,
+                                       packed=packed)
+    got = _np(out)
+    for b in range(B):
+        want = oracle.attention_decode_baseline(qo[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv, D, max_seq,
+                                                int(pos[b]) + 1)[0]
+        assert _relerr(got[b], want) <= TOL, f"sequence {b}"
+    if packed:
+        assert np.array_equal(_np(gate), gw)
+    kc_h, vc_h = _np(kc_d), _np(vc_d)
+    for b in range(B):
+        p = int(pos[b])
+        assert np.array_equal(vc_h[b, :, p], v[b])
+        _agree(kc_h[b, :, p], ko[b])
+    # the two-launch path gives the same attention output
+    kc2, vc2 = _t(dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))), _t(dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D)))
+    q2, k2 = _t(q), _t(k)
+    pr = aila_amd.decode_prepare_qkv(q2, k2, _t(v), _t(qw), _t(kw), None, None, pos=int(pos[0]),
+                                     positions=_t(pos) if device_pos else None, rotary_dim=rot, theta=theta,
+                                     eps=eps, packed_gate=packed)
+    q_prep = pr[0] if packed else pr
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out2 = aila_amd.gqa_decode_append(q_prep, k2, _t(v), kc2, vc2, int(pos.max()), workspace=ws,
+                                      positions=_t(pos) if device_pos else None)
+    torch.cuda.synchronize()
+    _agree(got, _np(out2))
