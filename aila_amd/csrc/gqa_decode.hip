@@ -428,40 +428,63 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
   __shared__ float s_f[kMaxSplits];
   __shared__ float s_inv;
   __shared__ f32x4 s_red[P][C4];
-  // One wave computes the split factors.
-  if (threadIdx.x < 64) {
-    float M = -INFINITY;
-    for (int i = threadIdx.x; i < ns; i += 64) M = fmaxf(M, rec0[static_cast<size_t>(i) * (kRecHeader + D)]);
-    M = fmaxf(M, __shfl_xor(M, 32));
-    M = fmaxf(M, __shfl_xor(M, 16));
-    M = row16_max(M);
-    float Ls = 0.f;
-    for (int i = threadIdx.x; i < ns; i += 64) {
-      const float* r = rec0 + static_cast<size_t>(i) * (kRecHeader + D);
-      const float f = (r[0] == -INFINITY) ? 0.f : expf(r[0] - M);
-      s_f[i] = f;
-      Ls += f * r[1];
-    }
-    Ls = wave_sum(Ls);
-    if (threadIdx.x == 0) s_inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-  }
-  __syncthreads();
   const int c = threadIdx.x % C4, ph = threadIdx.x / C4;
-  f32x4 a = {0.f, 0.f, 0.f, 0.f};
   constexpr int U = 8;
-  for (int i0 = ph; i0 < ns; i0 += P * U) {
-    f32x4 v[U];
+  // This thread's accumulator rows of the first P*U splits go out before the
+  // split factors, so the two rounds of loads overlap.
+  auto load_acc = [&](int i0, f32x4 (&v)[U]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = i0 + u * P;
       v[u] = (i < ns) ? *reinterpret_cast<const f32x4*>(rec0 + static_cast<size_t>(i) * (kRecHeader + D) + kRecHeader + 4 * c)
                       : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  };
+  f32x4 v[U];
+  load_acc(ph, v);
+  // One wave computes the split factors (m and l of each record in one
+  // load round: at most kMaxSplits / 64 records per lane).
+  if (threadIdx.x < 64) {
+    constexpr int kPerLane = kMaxSplits / 64;
+    float mv[kPerLane], lv[kPerLane];
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int i = threadIdx.x + 64 * j;
+      mv[j] = -INFINITY;
+      lv[j] = 0.f;
+      if (i < ns) {
+        const float* r = rec0 + static_cast<size_t>(i) * (kRecHeader + D);
+        mv[j] = r[0];
+        lv[j] = r[1];
+      }
+      M = fmaxf(M, mv[j]);
+    }
+    M = fmaxf(M, __shfl_xor(M, 32));
+    M = fmaxf(M, __shfl_xor(M, 16));
+    M = row16_max(M);
+    float Ls = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int i = threadIdx.x + 64 * j;
+      const float f = (mv[j] == -INFINITY) ? 0.f : expf(mv[j] - M);
+      if (i < ns) s_f[i] = f;
+      Ls += f * lv[j];
+    }
+    Ls = wave_sum(Ls);
+    if (threadIdx.x == 0) s_inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+  }
+  __syncthreads();
+  f32x4 a = {0.f, 0.f, 0.f, 0.f};
+  for (int i0 = ph;; ) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = i0 + u * P;
       if (i < ns) a += s_f[i] * v[u];
     }
+    i0 += P * U;
+    if (i0 >= ns) break;
+    load_acc(i0, v);
   }
   s_red[ph][c] = a;
   __syncthreads();
