@@ -14,7 +14,7 @@
 // reduced over the row groups of a wave with lane swaps and over the 4
 // waves through LDS. The narrower slab (CQ = 16) doubles the workgroups for
 // small batches, where one workgroup per CU leaves the state load latency
-// exposed (config-5 DeltaNet layer shape, B = 8: 7.14 -> 6.70 us).
+// exposed (Hv = 32, dk = dv = 128, B = 8: 7.14 -> 6.70 us).
 #include "common.hpp"
 
 #include <type_traits>
