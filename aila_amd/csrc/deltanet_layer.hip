@@ -194,23 +194,41 @@ __global__ __launch_bounds__(256 * G) void deltanet_layer_decode_kernel(
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
 // ---- prefill: causal conv + SiLU over T tokens into split planes ----------
-// Thread = 4 consecutive channels (never straddling the q/k/v boundaries,
-// all multiples of 4) over kConvTok consecutive tokens, with the three
-// previous raw rows in registers. History before token 0 is the ring:
-// h(-3) = ring[head], h(-2) = ring[head+1], h(-1) = ring[head+2].
-// Outputs: q as bf16; k and v as bf16 hi and bf16 residual lo planes, so
-// that hi + lo carries the fp32 activation to 2^-16 relative. The first
-// token block also writes the new ring (the last three raw rows, oldest at
-// row (head + T) % 3): it is the only block that reads or writes the ring.
-constexpr int kConvTok = 32;
+// Thread = CPT consecutive channels (8 when the rows allow 16-byte access,
+// else 4; never straddling the q/k/v boundaries, all multiples of 8) over
+// kConvTok consecutive tokens, with the three previous raw rows in
+// registers. History before token 0 is the ring: h(-3) = ring[head],
+// h(-2) = ring[head+1], h(-1) = ring[head+2]. Outputs: q as bf16; k and v
+// as bf16 hi and bf16 residual lo planes, so that hi + lo carries the fp32
+// activation to 2^-16 relative. The first token block also writes the new
+// ring (the last three raw rows, oldest at row (head + T) % 3): it is the
+// only block that reads or writes the ring.
+constexpr int kConvTok = 16;
 constexpr int kConvBatch = 8;   // rows loaded together before they are used
 
+template <int CPT>
+struct ConvVec;
+template <>
+struct ConvVec<4> { using raw = uint2; };
+template <>
+struct ConvVec<8> { using raw = u32x4; };
+
+template <int CPT>
+__device__ __forceinline__ void unpack_bf16(const typename ConvVec<CPT>::raw& r, float (&x)[CPT]) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&r);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) x[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+}
+
+template <int CPT>
 __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
     const bf16* __restrict__ qkv, int qkv_stride, const bf16* __restrict__ conv_w, float* __restrict__ conv_state,
     int conv_head, bf16* __restrict__ q_hi, bf16* __restrict__ k_hi, bf16* __restrict__ k_lo,
     bf16* __restrict__ v_hi, bf16* __restrict__ v_lo, int T, int qd, int vd) {
+  using Raw = typename ConvVec<CPT>::raw;
+  constexpr int NW = CPT / 2;          // 32-bit words per CPT bf16
   const int ch = 2 * qd + vd;
-  const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * CPT;
   if (c >= ch) return;
   const int b = blockIdx.z;
   const int tb0 = blockIdx.y * kConvTok;
@@ -219,34 +237,45 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
   const bf16* xb = qkv + static_cast<size_t>(b) * T * qkv_stride + c;
   float* ring = conv_state + static_cast<size_t>(b) * kRows * ch + c;
 
-  // taps: w[c+i][j] for the 4 channels
-  const u32x4 w01 = *reinterpret_cast<const u32x4*>(conv_w + static_cast<size_t>(c) * kConvK);
-  const u32x4 w23 = *reinterpret_cast<const u32x4*>(conv_w + static_cast<size_t>(c) * kConvK + 8);
-  float w[4][4];
+  // taps: w[c+i][j] for the CPT channels (CPT * 4 bf16, 16-byte loads)
+  float w[CPT][4];
   {
-    const uint32_t ww[8] = {w01[0], w01[1], w01[2], w01[3], w23[0], w23[1], w23[2], w23[3]};
+    uint32_t ww[CPT * 2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int v4 = 0; v4 < CPT / 2; ++v4) {   // 16 bytes = the taps of two channels
+      const u32x4 r = *reinterpret_cast<const u32x4*>(conv_w + static_cast<size_t>(c) * kConvK + v4 * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ww[v4 * 4 + e] = r[e];
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t word = ww[(i * 4 + j) >> 1];
         w[i][j] = __uint_as_float(((i * 4 + j) & 1) ? (word & 0xffff0000u) : (word << 16));
       }
   }
+  struct Row { float v[CPT]; };
   auto load_x = [&](int t) __attribute__((always_inline)) {
-    const uint2 r = *reinterpret_cast<const uint2*>(xb + static_cast<size_t>(t) * qkv_stride);
-    return f32x4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
-                 __uint_as_float(r.y & 0xffff0000u)};
+    Row r;
+    unpack_bf16<CPT>(*reinterpret_cast<const Raw*>(xb + static_cast<size_t>(t) * qkv_stride), r.v);
+    return r;
   };
-  f32x4 old_ring[kRows];
+  Row old_ring[kRows];
   auto hist = [&](int i) __attribute__((always_inline)) {   // raw row i (i >= -3)
     return i < 0 ? old_ring[i + kRows] : load_x(i);
   };
   if (tb0 == 0) {
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) old_ring[j] = *reinterpret_cast<const f32x4*>(ring + static_cast<size_t>((head + j) % kRows) * ch);
+    for (int j = 0; j < kRows; ++j)
+#pragma unroll
+      for (int v4 = 0; v4 < CPT / 4; ++v4) {
+        const f32x4 r = *reinterpret_cast<const f32x4*>(ring + static_cast<size_t>((head + j) % kRows) * ch + v4 * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) old_ring[j].v[v4 * 4 + e] = r[e];
+      }
   }
-  f32x4 h0 = hist(tb0 - 3), h1 = hist(tb0 - 2), h2 = hist(tb0 - 1);
+  Row h0 = hist(tb0 - 3), h1 = hist(tb0 - 2), h2 = hist(tb0 - 1);
   // destination plane and column
   const bool is_q = c < qd, is_k = !is_q && c < 2 * qd;
   const int width = (c < 2 * qd) ? qd : vd;
@@ -255,33 +284,38 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
   bf16* lo_plane = is_k ? k_lo : v_lo;
   for (int tb = tb0; tb < tend; tb += kConvBatch) {
     // a batch of rows in flight at once (clamped, so the loads stay unconditional)
-    f32x4 xs[kConvBatch];
+    Row xs[kConvBatch];
 #pragma unroll
     for (int i = 0; i < kConvBatch; ++i) xs[i] = load_x(min(tb + i, T - 1));
 #pragma unroll
     for (int u = 0; u < kConvBatch; ++u) {
       const int t = tb + u;
       if (t >= tend) break;
-      const f32x4 x = xs[u];
-      float y[4], r[4];
+      const Row& x = xs[u];
+      float y[CPT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float acc = h0[i] * w[i][0];
-        acc += h1[i] * w[i][1];
-        acc += h2[i] * w[i][2];
-        acc += x[i] * w[i][3];
+      for (int i = 0; i < CPT; ++i) {
+        float acc = h0.v[i] * w[i][0];
+        acc += h1.v[i] * w[i][1];
+        acc += h2.v[i] * w[i][2];
+        acc += x.v[i] * w[i][3];
         y[i] = silu_f(acc);
       }
-      const uint2 hw = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-      const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
-      *reinterpret_cast<uint2*>(hi_plane + o) = hw;
-      if (!is_q) {
+      Raw hw, lw;
+      uint32_t* hp = reinterpret_cast<uint32_t*>(&hw);
+      uint32_t* lp = reinterpret_cast<uint32_t*>(&lw);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t word = i < 2 ? hw.x : hw.y;
-          r[i] = y[i] - __uint_as_float((i & 1) ? (word & 0xffff0000u) : (word << 16));
-        }
-        *reinterpret_cast<uint2*>(lo_plane + o) = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+      for (int e = 0; e < NW; ++e) hp[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
+      const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
+      *reinterpret_cast<Raw*>(hi_plane + o) = hw;
+      if (!is_q) {
+        float r[CPT];
+#pragma unroll
+        for (int i = 0; i < CPT; ++i)
+          r[i] = y[i] - __uint_as_float((i & 1) ? (hp[i >> 1] & 0xffff0000u) : (hp[i >> 1] << 16));
+#pragma unroll
+        for (int e = 0; e < NW; ++e) lp[e] = pack_bf16x2(r[2 * e], r[2 * e + 1]);
+        *reinterpret_cast<Raw*>(lo_plane + o) = lw;
       }
       h0 = h1;
       h1 = h2;
@@ -290,11 +324,15 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
   }
   if (tb0 == 0) {
     // the ring after T tokens: raw rows T-3, T-2, T-1 at rows (head + T + j) % 3
-    f32x4 nr[kRows];
+    Row nr[kRows];
 #pragma unroll
     for (int j = 0; j < kRows; ++j) nr[j] = hist(T - kRows + j);
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) *reinterpret_cast<f32x4*>(ring + static_cast<size_t>((head + T + j) % kRows) * ch) = nr[j];
+    for (int j = 0; j < kRows; ++j)
+#pragma unroll
+      for (int v4 = 0; v4 < CPT / 4; ++v4)
+        *reinterpret_cast<f32x4*>(ring + static_cast<size_t>((head + T + j) % kRows) * ch + v4 * 4) =
+            f32x4{nr[j].v[v4 * 4], nr[j].v[v4 * 4 + 1], nr[j].v[v4 * 4 + 2], nr[j].v[v4 * 4 + 3]};
   }
 }
 
@@ -396,10 +434,18 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   auto plane = [&](size_t off) { return reinterpret_cast<bf16*>(ws + off); };
-  const dim3 cgrid((ch / 4 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
-  hipLaunchKernelGGL(deltanet_conv_split_kernel, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv), qkv_stride,
-                     static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi), plane(w.k_hi),
-                     plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
+  // 16-byte row access when the fused rows allow it
+  if (aligned(qkv, 16) && qkv_stride % 8 == 0) {
+    const dim3 cgrid((ch / 8 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
+    hipLaunchKernelGGL(deltanet_conv_split_kernel<8>, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv),
+                       qkv_stride, static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi),
+                       plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
+  } else {
+    const dim3 cgrid((ch / 4 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
+    hipLaunchKernelGGL(deltanet_conv_split_kernel<4>, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv),
+                       qkv_stride, static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi),
+                       plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
+  }
   launch_deltanet_chunked(plane(w.q_hi), plane(w.k_hi), plane(w.v_hi), plane(w.k_lo), plane(w.v_lo),
                           static_cast<const bf16*>(a), static_cast<const bf16*>(b), ab_stride,
                           static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out), ws + w.records,

@@ -163,6 +163,28 @@ def test_layer_prefill_matches_oracle(B, T, Hk, Hv, head0, slow):
     assert np.array_equal(_np(cs), want_cs), "conv ring must hold the last raw inputs bit-exact"
 
 
+def test_layer_prefill_odd_qkv_row_stride():
+    """qkv rows padded to ch + 4 elements (a row stride that is not a
+    multiple of 8): the conv pass takes its 8-byte path instead of the
+    16-byte one; same results."""
+    import torch
+    import aila_amd
+    B, T, Hk, Hv, head0, d = 2, 100, 2, 4, 1, 128
+    x = _inputs(975, B, T, Hk, Hv)
+    want_out, want_S, want_cs = _oracle(x, B, T, Hk, Hv, head0)
+    ch = 2 * Hk * d + Hv * d
+    padded = np.zeros((B, T, ch + 4), np.uint16)
+    padded[..., :ch] = x["qkv"]
+    qkv = _t(padded)[:, :, :ch]
+    st, cs = _t(x["state"]), _t(x["conv_state"])
+    out = aila_amd.deltanet_layer_prefill(qkv, _t(x["z"]), _t(x["a"]), _t(x["b"]), _t(x["conv_w"]), cs, head0,
+                                          _t(x["norm_w"]), st, Hk, dt_bias=_t(x["dt_bias"]), A_log=_t(x["A_log"]))
+    torch.cuda.synchronize()
+    assert _rel(_np(st), want_S) <= STATE_TOL
+    assert _rel(dg.bf16_to_f32(_np(out)), dg.bf16_to_f32(want_out)) <= OUT_TOL
+    assert np.array_equal(_np(cs), want_cs)
+
+
 def test_layer_prefill_fused_rows_then_decode():
     """Prefill from the backend's fused [qkv | z | a | b] rows, then decode
     steps continuing the same ring and state; all against one oracle run."""
