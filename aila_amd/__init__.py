@@ -483,7 +483,9 @@ def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_
                               out=None, gate_out=None, workspace=None, positions=None, stream=None):
     """QK-norm + RoPE + K/V append + split-K decode in one launch.
     q_in [B,Hq,D] (or [B,Hq,2D] q|gate when packed_gate); k_new/v_new [B,Hkv,D];
-    caches [B,Hkv,max_seq,D]. Returns out (and gate_out when packed)."""
+    caches [B,Hkv,max_seq,D]. Returns out (and gate_out when packed).
+    Without a workspace the decode runs single-pass (one workgroup per KV
+    head), as gqa_decode_append."""
     import torch
     B, Hkv, max_seq, D = k_cache.shape
     Hq = q_in.shape[1]
@@ -502,14 +504,17 @@ def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_
         if gate_out is None:
             gate_out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k_cache.device)
         _need(gate_out, torch.bfloat16, (B, Hq, D), "gate_out")
-    if workspace is None:
-        workspace = torch.empty(gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device=k_cache.device)
+    ws_bytes = 0
+    if workspace is not None:
+        if not workspace.is_cuda or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous device tensor")
+        ws_bytes = workspace.numel() * workspace.element_size()
     if positions is not None:
         _need(positions, torch.int32, (B,), "positions", align=4)
     rc = lib().aila_hip_gqa_decode_prepare_append(
         _ptr(q_in), int(bool(packed_gate)), _ptr(gate_out) if packed_gate else None, _ptr(k_new), _ptr(v_new),
         _ptr(q_norm_w), _ptr(k_norm_w), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(workspace),
-        workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, max_seq,
+        ws_bytes, B, Hq, Hkv, D, max_seq,
         D if rotary_dim is None else int(rotary_dim), float(theta), float(eps), int(pos), _ptr(positions),
         _stream(stream))
     _check(rc, "gqa_decode_prepare_append")

@@ -150,15 +150,16 @@ def test_sigmoid_mul(n):
     assert np.array_equal(_np(out), _np(xd))
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,rot,packed,device_pos", [
-    (3, 16, 4, 256, 64, True, True),     # Qwen3.5 attention layer
-    (2, 16, 8, 128, 128, False, False),  # Qwen3
-    (2, 8, 1, 128, 32, True, True),      # narrow rotary, eight heads per group
+@pytest.mark.parametrize("B,Hq,Hkv,D,rot,packed,device_pos,split", [
+    (3, 16, 4, 256, 64, True, True, True),     # Qwen3.5 attention layer
+    (2, 16, 8, 128, 128, False, False, True),  # Qwen3
+    (2, 8, 1, 128, 32, True, True, True),      # narrow rotary, eight heads per group
+    (3, 16, 4, 256, 64, True, True, False),    # no workspace: single pass
 ])
-def test_fused_prepare_append_decode(B, Hq, Hkv, D, rot, packed, device_pos):
-    """One launch (QK-norm + RoPE + append + split-K decode) against the
-    oracle's prep followed by its attention, and against the two-launch
-    path (decode_prepare_qkv + gqa_decode_append)."""
+def test_fused_prepare_append_decode(B, Hq, Hkv, D, rot, packed, device_pos, split):
+    """One launch (QK-norm + RoPE + append + split-K or single-pass decode)
+    against the oracle's prep followed by its attention, and against the
+    two-launch path (decode_prepare_qkv + gqa_decode_append)."""
     import torch
     import aila_amd
     seed, theta, eps, max_seq = 760 + D, 1e7, 1e-6, 2048
@@ -171,9 +172,10 @@ def test_fused_prepare_append_decode(B, Hq, Hkv, D, rot, packed, device_pos):
     kc = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
     vc = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
     kc_d, vc_d = _t(kc), _t(vc)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda") if split else None
     res = aila_amd.gqa_decode_prepare_append(
         _t(q), _t(k), _t(v), kc_d, vc_d, int(pos.max()), q_norm_w=_t(qw), k_norm_w=_t(kw), rotary_dim=rot,
-        theta=theta, eps=eps, packed_gate=packed, positions=_t(pos) if device_pos else None)
+        theta=theta, eps=eps, packed_gate=packed, positions=_t(pos) if device_pos else None, workspace=ws)
     torch.cuda.synchronize()
     out, gate = res if packed else (res, None)
     # oracle: prep, append, attention per sequence
