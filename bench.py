@@ -403,6 +403,53 @@ def sub_deltanet_prefill(torch, aila_amd, reps=10):
             "tok_per_s": round(T / (us * 1e-6)), "roofline_frac": round(frac, 4)}
 
 
+def sub_fused_prep_decode(torch, aila_amd, per_graph=8, reps=8):
+    """One config-5 GQA layer step (B=8, Hq=16, Hkv=4, D=256, rotary 64,
+    packed q|gate, context 32768): the one-launch prep + append + decode
+    against the two launches decode_prepare_qkv + gqa_decode_append."""
+    B, Hq, Hkv, D, rot, L = B5, GQA_HQ, GQA_HKV, GQA_D, 64, 32768
+    max_seq = L + 1024
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 7)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    kc = torch.empty((B, Hkv, max_seq, D), **bf).normal_(generator=g)
+    vc = torch.empty_like(kc).normal_(generator=g)
+    qg = torch.randn((B, Hq, 2 * D), generator=g, **bf)
+    k = torch.randn((B, Hkv, D), generator=g, **bf)
+    v = torch.randn((B, Hkv, D), generator=g, **bf)
+    wq, wk = torch.randn(D, generator=g, **bf), torch.randn(D, generator=g, **bf)
+    pos = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out, go, qo = (torch.empty((B, Hq, D), **bf) for _ in range(3))
+    kk = torch.empty_like(k)
+
+    def fused():
+        aila_amd.gqa_decode_prepare_append(qg, k, v, kc, vc, L, q_norm_w=wq, k_norm_w=wk, rotary_dim=rot,
+                                           theta=1e7, packed_gate=True, out=out, gate_out=go, workspace=ws,
+                                           positions=pos)
+
+    def two():
+        kk.copy_(k)   # decode_prepare_qkv normalises and rotates k in place
+        aila_amd.decode_prepare_qkv(qg, kk, v, wq, wk, None, None, positions=pos, rotary_dim=rot, theta=1e7,
+                                    packed_gate=True, q_out=qo, gate_out=go)
+        aila_amd.gqa_decode_append(qo, kk, v, kc, vc, L, out=out, workspace=ws, positions=pos)
+
+    res = {}
+    for name, fn in (("fused_us", fused), ("two_launch_us", two)):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(per_graph):
+                fn()
+        gr.replay()
+        res[name] = round(time_graph(torch, gr, reps) * 1e3 / per_graph, 2)
+    del kc, vc
+    res["config"] = "config-5 GQA layer step B=8 Hq=16 Hkv=4 D=256 L=32768, prep + append + decode"
+    res["two_launch_note"] = "includes a 32 KiB device copy of k (the two-launch prep rotates k in place)"
+    return res
+
+
 def sub_decode_prep(torch, aila_amd, per_graph=32, reps=20):
     """QK-norm + partial RoPE + packed q|gate split + K/V append for one
     config-5 GQA layer (B=8, Hq=16, Hkv=4, D=256, rotary 64)."""
@@ -546,7 +593,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
                     choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill",
-                             "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep"],
+                             "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     args = ap.parse_args()
@@ -566,7 +613,8 @@ def main():
          "deltanet_prefill": lambda t, a: sub_deltanet_prefill(t, a, reps=20),
          "deltanet_layer_decode": lambda t, a: sub_deltanet_layer_decode(t, a, steps=320),
          "deltanet_layer_prefill": lambda t, a: sub_deltanet_layer_prefill(t, a, reps=10),
-         "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20)}[args.profile_kernel](torch, aila_amd)
+         "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20),
+         "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a)}[args.profile_kernel](torch, aila_amd)
         if r:
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
         return
@@ -593,6 +641,8 @@ def main():
         sub["gqa_decode_cfg1"] = sub_decode_cfg1(torch, aila_amd)
         sub["decode_prep"] = sub_decode_prep(torch, aila_amd)
         log(f"[bench] decode prep {sub['decode_prep']}")
+        sub["fused_prep_decode"] = sub_fused_prep_decode(torch, aila_amd)
+        log(f"[bench] fused prep+decode {sub['fused_prep_decode']}")
         log(f"[bench] decode cfg1 {sub['gqa_decode_cfg1']}")
     cpu = None
     if not args.no_cpu:
