@@ -24,6 +24,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace aila {
@@ -537,19 +538,22 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
 // one such round: with L=32768, B=8, Hkv=4, D=256 measured 6.45 TB/s for
 // 512 workgroups (2 per CU) against 5.91 for 2048 and 5.97 for 768 (every
 // extra round pays the workgroup start-up latency and a partial tail).
+// The per-device value is idempotent, so concurrent first calls may both
+// compute it; the atomic makes the publication race-free.
 template <int D, int G>
 int resident_workgroups() {
   constexpr int kMaxDev = 64;
-  static int cache[kMaxDev] = {};
+  static std::atomic<int> cache[kMaxDev];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 512;
-  if (cache[dev] > 0) return cache[dev];
+  const int known = cache[dev].load(std::memory_order_relaxed);
+  if (known > 0) return known;
   int per_cu = 0, cus = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gqa_decode_split_kernel<D, G>, kThreads, 0) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
     return 512;
-  cache[dev] = per_cu * cus;
-  return cache[dev];
+  cache[dev].store(per_cu * cus, std::memory_order_relaxed);
+  return per_cu * cus;
 }
 
 int resident_for(int D, int G) {

@@ -76,3 +76,6 @@ class Context {
 };
 
 }  // namespace aila
+
+// The reference's Context is a global class (src/core/Context.hpp:14).
+using aila::Context;

@@ -9,7 +9,11 @@
 #include "Context.hpp"
 #include "Tensor.hpp"
 
-namespace aila {
+// The reference declares these at top level (namespace ops, Ops.hpp:139)
+// over global Context and Tensor classes (src/core/Context.hpp:14,
+// Tensor.hpp:15); Context.hpp and Tensor.hpp here export aila::Context and
+// aila::Tensor at global scope, so the backends' unqualified
+// ops::attention_decode(ctx, ...) calls bind unchanged.
 namespace ops {
 
 // new_kv [seq_len, num_heads*head_dim] -> cache [num_heads, max_seq_len,
@@ -153,4 +157,3 @@ void linear_delta_layer_prefill(Context& ctx, Tensor& fused_all, Tensor& out, in
                                 int num_v_heads, int head_k_dim, int head_v_dim, int conv_kernel, float eps);
 
 }  // namespace ops
-}  // namespace aila

@@ -94,3 +94,7 @@ class Tensor {
 };
 
 }  // namespace aila
+
+// The reference's Tensor is a global class (src/core/Tensor.hpp:15).
+using aila::DType;
+using aila::Tensor;

@@ -8,7 +8,6 @@
 
 #include "aila_hip.h"
 
-namespace aila {
 namespace ops {
 namespace {
 
@@ -275,4 +274,3 @@ void linear_delta_layer_prefill(Context& ctx, Tensor& fused_all, Tensor& out, in
 }
 
 }  // namespace ops
-}  // namespace aila

@@ -25,6 +25,8 @@ void orc_apply_rope(uint16_t*, uint16_t*, int, int, int, int, int, int, float);
 void orc_decode_prepare(const uint16_t*, int, uint16_t*, uint16_t*, uint16_t*, const uint16_t*, const uint16_t*,
                         const uint16_t*, uint16_t*, uint16_t*, int, int, int, int, int, int, float, float,
                         const int*);
+void orc_decode_prepare_qkv(uint16_t*, uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*,
+                            uint16_t*, int, int, int, int, float, float, int);
 void orc_sigmoid_mul(const uint16_t*, const uint16_t*, uint16_t*, long);
 void orc_deltanet_layer(const uint16_t*, int, const uint16_t*, int, const uint16_t*, const uint16_t*, int,
                         const uint16_t*, float*, int, const uint16_t*, const float*, const float*, float*, uint16_t*,
@@ -33,7 +35,6 @@ uint16_t orc_f32_to_bf16(float);
 float orc_bf16_to_f32(uint16_t);
 }
 
-using namespace aila;
 using u16v = std::vector<uint16_t>;
 
 static int g_fail = 0;
@@ -84,6 +85,63 @@ static std::vector<T> download(Context& ctx, Tensor& t) {
   ctx.memcpy_d2h(h.data(), t.data(), h.size() * sizeof(T));
   return h;
 }
+
+// A backend-shaped caller: the per-layer attention statements of a dense
+// Qwen3 backend (Qwen3DenseBackend.cpp:293-347) use unqualified ops:: calls
+// on a global Context and Tensor, a KV cache object with k_cache(i) /
+// v_cache(i) / max_length() and a config struct. They bind here unchanged.
+namespace backend_shape {
+struct Config {
+  int num_attention_heads, num_key_value_heads, head_dim;
+  float rms_norm_eps, rope_theta;
+};
+struct LayerCache {
+  std::vector<Tensor> k, v;
+  int max_len;
+  Tensor& k_cache(int i) { return k[i]; }
+  Tensor& v_cache(int i) { return v[i]; }
+  int max_length() const { return max_len; }
+};
+struct Buffers {
+  Tensor q, k, v, attn_out, scores, decode_scores, rope_freq;
+};
+struct Layer {
+  Tensor* q_norm_weight;
+  Tensor* k_norm_weight;
+};
+
+// One layer's attention for seq_len tokens at start_pos, written as the
+// backend writes it.
+void attention_layer(Context& ctx, const Config& cfg_, LayerCache& kv_cache_, Buffers& buf_, Layer& layer, int i,
+                     int seq_len, int start_pos) {
+  if (seq_len == 1) {
+    ops::decode_prepare_qkv(ctx, buf_.q, buf_.k, buf_.v, buf_.rope_freq, *layer.q_norm_weight, *layer.k_norm_weight,
+                            kv_cache_.k_cache(i), kv_cache_.v_cache(i), start_pos, cfg_.num_attention_heads,
+                            cfg_.num_key_value_heads, cfg_.head_dim, cfg_.rms_norm_eps, cfg_.rope_theta);
+    ops::attention_decode(ctx, buf_.q, kv_cache_.k_cache(i), kv_cache_.v_cache(i), buf_.attn_out,
+                          buf_.decode_scores, cfg_.num_attention_heads, cfg_.num_key_value_heads, cfg_.head_dim,
+                          start_pos + 1);
+    return;
+  }
+  ops::head_rms_norm(ctx, buf_.q, *layer.q_norm_weight, cfg_.rms_norm_eps, seq_len, cfg_.num_attention_heads,
+                     cfg_.head_dim);
+  ops::head_rms_norm(ctx, buf_.k, *layer.k_norm_weight, cfg_.rms_norm_eps, seq_len, cfg_.num_key_value_heads,
+                     cfg_.head_dim);
+  ops::apply_rope(ctx, buf_.q, buf_.k, seq_len, start_pos, cfg_.num_attention_heads, cfg_.num_key_value_heads,
+                  cfg_.head_dim, cfg_.rope_theta);
+  ops::copy_to_cache(ctx, buf_.k, kv_cache_.k_cache(i), seq_len, start_pos, cfg_.num_key_value_heads, cfg_.head_dim,
+                     kv_cache_.max_length());
+  ops::copy_to_cache(ctx, buf_.v, kv_cache_.v_cache(i), seq_len, start_pos, cfg_.num_key_value_heads, cfg_.head_dim,
+                     kv_cache_.max_length());
+  if (start_pos == 0)
+    ops::attention_prefill(ctx, buf_.q, buf_.k, buf_.v, buf_.attn_out, buf_.scores, seq_len,
+                           cfg_.num_attention_heads, cfg_.num_key_value_heads, cfg_.head_dim);
+  else
+    ops::attention_prefill_cached(ctx, buf_.q, kv_cache_.k_cache(i), kv_cache_.v_cache(i), buf_.attn_out,
+                                  buf_.scores, seq_len, start_pos, cfg_.num_attention_heads,
+                                  cfg_.num_key_value_heads, cfg_.head_dim, kv_cache_.max_length());
+}
+}  // namespace backend_shape
 
 int main() {
   Context ctx;
@@ -300,6 +358,65 @@ int main() {
     const double eo = relerr(download<uint16_t>(ctx, out), ow);
     expect(es <= 1e-3 && eo <= 1e-2 && download<float>(ctx, tcs) == csw && head == (1 + T) % 3,
            "linear_delta_layer prefill + decode", std::fmax(es, eo));
+  }
+  // ---- the backend-shaped caller: prefill 40 tokens, then decode one ------
+  {
+    using namespace backend_shape;
+    const Config cfg{16, 8, 128, 1e-6f, 1e6f};
+    const int Hq = 16, Hkv = 8, D = 128, max_seq = 96, S = 40;
+    LayerCache kv;
+    kv.max_len = max_seq;
+    kv.k.push_back(Tensor::allocate(ctx, {Hkv, max_seq, D}));
+    kv.v.push_back(Tensor::allocate(ctx, {Hkv, max_seq, D}));
+    u16v qw = rand_bf16(D), kw = rand_bf16(D);
+    Tensor tqw = upload(ctx, qw, {D}, DType::bf16), tkw = upload(ctx, kw, {D}, DType::bf16);
+    Layer layer{&tqw, &tkw};
+    u16v q = rand_bf16(size_t(S) * Hq * D), k = rand_bf16(size_t(S) * Hkv * D), v = rand_bf16(size_t(S) * Hkv * D);
+    Buffers buf;
+    buf.q = upload(ctx, q, {S, Hq * D}, DType::bf16);
+    buf.k = upload(ctx, k, {S, Hkv * D}, DType::bf16);
+    buf.v = upload(ctx, v, {S, Hkv * D}, DType::bf16);
+    buf.attn_out = Tensor::allocate(ctx, {S, Hq * D});
+    buf.scores = Tensor::allocate(ctx, {1}, DType::f32);
+    buf.decode_scores = Tensor::allocate(ctx, {Hq, max_seq}, DType::f32);
+    buf.rope_freq = Tensor::allocate(ctx, {D / 2}, DType::f32);
+    attention_layer(ctx, cfg, kv, buf, layer, 0, S, 0);
+    u16v got_pre = download<uint16_t>(ctx, buf.attn_out);
+    // oracle: norms, rope, cache, naive prefill
+    u16v wq = q, wk = k, ck(size_t(Hkv) * max_seq * D, 0), cv(size_t(Hkv) * max_seq * D, 0), want(size_t(S) * Hq * D);
+    orc_head_rms_norm(wq.data(), qw.data(), nullptr, cfg.rms_norm_eps, S, Hq, D);
+    orc_head_rms_norm(wk.data(), kw.data(), nullptr, cfg.rms_norm_eps, S, Hkv, D);
+    orc_apply_rope(wq.data(), wk.data(), S, 0, Hq, Hkv, D, D, cfg.rope_theta);
+    orc_copy_to_cache(wk.data(), ck.data(), S, 0, Hkv, D, max_seq);
+    orc_copy_to_cache(v.data(), cv.data(), S, 0, Hkv, D, max_seq);
+    orc_attention_prefill_naive(wq.data(), wk.data(), v.data(), want.data(), S, Hq, Hkv, D);
+    const double e1 = relerr(got_pre, want);
+    // decode token S through the same statements
+    u16v q1 = rand_bf16(size_t(Hq) * D), k1 = rand_bf16(size_t(Hkv) * D), v1 = rand_bf16(size_t(Hkv) * D);
+    buf.q = upload(ctx, q1, {1, Hq * D}, DType::bf16);
+    buf.k = upload(ctx, k1, {1, Hkv * D}, DType::bf16);
+    buf.v = upload(ctx, v1, {1, Hkv * D}, DType::bf16);
+    buf.attn_out = Tensor::allocate(ctx, {1, Hq * D});
+    attention_layer(ctx, cfg, kv, buf, layer, 0, 1, S);
+    u16v got_dec = download<uint16_t>(ctx, buf.attn_out);
+    u16v want_dec(size_t(Hq) * D);
+    orc_decode_prepare_qkv(q1.data(), k1.data(), v1.data(), qw.data(), kw.data(), ck.data(), cv.data(), S, Hq, Hkv,
+                           D, cfg.rms_norm_eps, cfg.rope_theta, max_seq);
+    orc_attention_decode_baseline(q1.data(), ck.data(), cv.data(), want_dec.data(), 1, Hq, Hkv, D, max_seq, S + 1);
+    const double e2 = relerr(got_dec, want_dec);
+    u16v gk = download<uint16_t>(ctx, kv.k_cache(0)), gv = download<uint16_t>(ctx, kv.v_cache(0));
+    // rows [0, S] of every head (rows past them were never written); the
+    // k rows went through the GPU's norm and rotation, so to tolerance
+    u16v rk, rv, wrk, wrv;
+    for (int h = 0; h < Hkv; ++h) {
+      const size_t o = size_t(h) * max_seq * D, n = size_t(S + 1) * D;
+      rk.insert(rk.end(), gk.begin() + o, gk.begin() + o + n);
+      wrk.insert(wrk.end(), ck.begin() + o, ck.begin() + o + n);
+      rv.insert(rv.end(), gv.begin() + o, gv.begin() + o + n);
+      wrv.insert(wrv.end(), cv.begin() + o, cv.begin() + o + n);
+    }
+    const bool cache_ok = relerr(rk, wrk) <= 1e-2 && rv == wrv;
+    expect(e1 <= 1e-2 && e2 <= 1e-2 && cache_ok, "backend-shaped ops:: caller (prefill, decode)", std::fmax(e1, e2));
   }
   std::printf("peak device bytes %zu\n", ctx.peak_allocated_bytes());
   std::printf(g_fail ? "FAILED %d\n" : "ALL OK\n", g_fail);
