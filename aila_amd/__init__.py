@@ -27,6 +27,8 @@ _SIGS = {
     "aila_hip_version": ([], _I),
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_gqa_decode_noalloc_max_bytes": ([], _SZ),
+    "aila_hip_gqa_decode_noalloc": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_decode_prepare_append": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I,
                                             _I, _F, _F, _I, _P, _P], _I),
@@ -141,6 +143,27 @@ def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
                                    _ptr(workspace), ws_bytes, B, Hq, Hkv, D, max_seq,
                                    int(cached_len), _ptr(seq_lens), _stream(stream))
     _check(rc, "aila_hip_gqa_decode")
+    return out
+
+
+def gqa_decode_noalloc(q, k_cache, v_cache, cached_len: int, out=None, seq_lens=None, stream=None):
+    """gqa_decode with the split records in the library's static device
+    scratch (no workspace argument, no allocation in the library). Calls
+    that overlap on one GPU share that scratch and race."""
+    import torch
+    B, Hq, D = q.shape
+    Hkv, max_seq = k_cache.shape[1], k_cache.shape[2]
+    _need(q, torch.bfloat16, (B, Hq, D), "q")
+    _need(k_cache, torch.bfloat16, (B, Hkv, max_seq, D), "k_cache")
+    _need(v_cache, torch.bfloat16, (B, Hkv, max_seq, D), "v_cache")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.bfloat16, (B, Hq, D), "out")
+    if seq_lens is not None:
+        _need(seq_lens, torch.int32, (B,), "seq_lens", align=4)
+    rc = lib().aila_hip_gqa_decode_noalloc(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), B, Hq, Hkv, D,
+                                           max_seq, int(cached_len), _ptr(seq_lens), _stream(stream))
+    _check(rc, "aila_hip_gqa_decode_noalloc")
     return out
 
 

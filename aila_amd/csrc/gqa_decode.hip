@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 namespace aila {
@@ -653,6 +654,72 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache, const voi
                                    int max_seq, int cached_len, const int* seq_lens, void* stream) {
   return aila::gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq,
                                cached_len, seq_lens, 0, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split records live in a file-scope device
+// array instead of a caller workspace. Its host-side name is only a stand-in
+// for the symbol, so every host use goes through the device address that
+// hipGetSymbolAddress returns, looked up once per device with that device
+// current and kept per device.
+namespace aila {
+namespace {
+constexpr size_t kScratchBytes = size_t(8) << 20;   // 8 MiB per device
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxScratchDev = 64;
+std::atomic<float*> g_scratch_ptr[kMaxScratchDev];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (null + error set on
+// failure).
+float* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDev) {
+    set_error(AILA_HIP_ELAUNCH, "gqa_decode_noalloc: no usable current device (%d)", dev);
+    return nullptr;
+  }
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (p) return p;
+  void* addr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || addr == nullptr) {
+    set_error(AILA_HIP_ELAUNCH, "gqa_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+              hipGetErrorString(e));
+    return nullptr;
+  }
+  p = static_cast<float*>(addr);
+  g_scratch_ptr[dev].store(p, std::memory_order_release);
+  return p;
+}
+}  // namespace
+}  // namespace aila
+
+extern "C" size_t aila_hip_gqa_decode_noalloc_max_bytes(void) { return aila::kScratchBytes; }
+
+extern "C" int aila_hip_gqa_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                           int B, int Hq, int Hkv, int D, int max_seq, int cached_len,
+                                           const int* seq_lens, void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(B > 0 && Hq > 0 && D > 0, "gqa_decode_noalloc: bad shape (B=%d Hq=%d D=%d)", B, Hq, D);
+  // Two split records per (sequence, head) is the least a split needs.
+  const size_t need = static_cast<size_t>(B) * Hq * 2 * (kRecHeader + D) * sizeof(float);
+  if (need > kScratchBytes)
+    return set_error(AILA_HIP_EINVAL,
+                     "gqa_decode_noalloc: B*Hq = %d heads of D = %d need %zu bytes of split records, above the "
+                     "static %zu-byte scratch; use aila_hip_gqa_decode with a workspace",
+                     B * Hq, D, need, kScratchBytes);
+  float* ws = scratch_for_current_device();
+  if (!ws) return AILA_HIP_ELAUNCH;
+  // As many records per (sequence, head) as the scratch holds (capped at
+  // the split limit); no record needs clearing: the merge reads only the
+  // splits that hold rows of the sequence, and each of those is written by
+  // its split workgroup in the same call.
+  return gqa_decode_impl(q, k_cache, v_cache, out, ws, kScratchBytes, B, Hq, Hkv, D, max_seq, cached_len, seq_lens,
+                         0, nullptr, nullptr, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int aila_hip_gqa_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache,

@@ -65,6 +65,23 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int B, int Hq, int Hkv, int D, int max_seq,
                         int cached_len, const int* seq_lens, void* stream);
 
+/* Allocation-free variant of aila_hip_gqa_decode. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory or pass a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). The split records live in a static device array
+ * of aila_hip_gqa_decode_noalloc_max_bytes() bytes (8 MiB) per GPU, held
+ * until the process ends; it calls no allocating routine. Sizes whose two
+ * split records per head exceed it (B*Hq*2*(16+D)*4 bytes > 8 MiB) are
+ * rejected with AILA_HIP_EINVAL. Every call on one GPU shares that array,
+ * so calls that overlap in time on the same GPU (different streams, or
+ * different threads) race: serialise them. Arguments and results as
+ * aila_hip_gqa_decode with a workspace. */
+size_t aila_hip_gqa_decode_noalloc_max_bytes(void);
+int aila_hip_gqa_decode_noalloc(const void* q, const void* k_cache,
+                                const void* v_cache, void* out, int B, int Hq,
+                                int Hkv, int D, int max_seq, int cached_len,
+                                const int* seq_lens, void* stream);
+
 /* Decode step with the new token's K/V append fused in (the cache write of
  * ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:105-216, followed by
  * ops::attention_decode with cached_len = start_pos + 1, as the backends call
