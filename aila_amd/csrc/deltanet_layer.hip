@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256 * G) void deltanet_layer_decode_kernel(
   f32x4 s[kRPT];
 #pragma unroll
   for (int r = 0; r < kRPT; ++r)
-    s[r] = *reinterpret_cast<const f32x4*>(S + static_cast<size_t>(rg * kRPT + r) * kD + col);
+    s[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + static_cast<size_t>(rg * kRPT + r) * kD + col));
 
   // 2. Convolution + SiLU into LDS; the new raw row replaces the oldest.
 #pragma unroll
@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256 * G) void deltanet_layer_decode_kernel(
   }
 #pragma unroll
   for (int r = 0; r < kRPT; ++r)
-    *reinterpret_cast<f32x4*>(S + static_cast<size_t>(rg * kRPT + r) * kD + col) = s[r];
+    __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4*>(S + static_cast<size_t>(rg * kRPT + r) * kD + col));
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], 32);
   if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[g][1][wave_in_head][cq * 4]) = o;

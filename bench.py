@@ -367,10 +367,37 @@ def sub_deltanet_layer_decode(torch, aila_amd, steps=512, per_graph=16):
             aila_amd.deltanet_decode(q[0], q[1], v, xs[0]["a"], xs[0]["b"], st, out=o2)
     gr2.replay()
     us2 = time_graph(torch, gr2, steps // per_graph) * 1e3 / per_graph
+    # As in the config-5 stack: 24 layers, each with its own state (403 MB
+    # in all), so every step finds its state evicted from the caches.
+    nl = N_LAYERS - N_GQA
+    sts = [torch.empty_like(st).normal_(0, 0.02, generator=g) for _ in range(nl)]
+    css = [torch.empty_like(cs).normal_(generator=g) for _ in range(nl)]
+    gr3 = torch.cuda.CUDAGraph()
+    gr4 = torch.cuda.CUDAGraph()
+    x0 = xs[0]
+    with torch.cuda.graph(gr3):
+        for i in range(nl):
+            aila_amd.deltanet_layer_decode(x0["qkv"], x0["z"], x0["a"], x0["b"], w, css[i], 0, nw, sts[i], Hk,
+                                           out=out, conv_heads=heads)
+    with torch.cuda.graph(gr4):
+        for i in range(nl):
+            aila_amd.deltanet_decode(q[0], q[1], v, x0["a"], x0["b"], sts[i], out=o2)
+    gr3.replay()
+    gr4.replay()
+    us3 = time_graph(torch, gr3, max(steps // nl, 8)) * 1e3 / nl
+    us4 = time_graph(torch, gr4, max(steps // nl, 8)) * 1e3 / nl
+    del sts, css
+    rb = deltanet_bytes(B, Hk, Hv, d, d)
     return {"config": f"layer decode B={B} Hk={Hk} Hv={Hv} d={d} (config-5 DeltaNet layer)",
             "us_per_step": round(us, 3), "GBps": round(byts / us / 1e3, 1),
             "x_of_bound": round(us / (byts / (HBM_PEAK_GBS * 1e3)), 3),
-            "recurrence_only_us": round(us2, 3)}
+            "recurrence_only_us": round(us2, 3),
+            "recurrence_only_x_of_bound": round(us2 / (rb / (HBM_PEAK_GBS * 1e3)), 3),
+            "state_evicted_us": round(us3, 3),
+            "state_evicted_x_of_bound": round(us3 / (byts / (HBM_PEAK_GBS * 1e3)), 3),
+            "state_evicted_recurrence_only_us": round(us4, 3),
+            "state_evicted_recurrence_only_x_of_bound": round(us4 / (rb / (HBM_PEAK_GBS * 1e3)), 3),
+            "state_evicted_note": "24 states in rotation, one per DeltaNet layer of the config-5 stack"}
 
 
 def sub_deltanet_prefill(torch, aila_amd, reps=10):
@@ -583,6 +610,74 @@ def cpu_baseline(min_seconds=10.0):
             "seconds_per_group": round(t, 4)}
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_configs(runs=5):
+    """The reference math (the scalar oracle, fast-math build, OpenMP) on the
+    host cores for configs 2, 3 and 4, median of `runs` runs after one
+    warm-up each. Baseline, not target. Config 2 runs the reference's naive
+    3-pass prefill (AttentionOps.cpp:769-841) on the first 1024 tokens (a
+    quarter of the causal FLOPs) and reports the FLOP rate; configs 3 and 4
+    run the sequential recurrence (Qwen35HybridTextBackend.cpp:1729-1780)
+    at full shape (config 3: 16 steps per run)."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(0xA11A)
+
+    def bf16(shape):
+        x = rng.standard_normal(int(np.prod(shape)), dtype=np.float32)
+        return (x.view(np.uint32) >> 16).astype(np.uint16).reshape(shape)
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    threads = oracle.num_threads(fast=True)
+    res = {"note": "baseline, not target", "cpu_model": cpu_model(), "threads": threads, "runs": runs,
+           "build": "oracle/liboracle_fast.so (-O3 -ffast-math, OpenMP)"}
+    # config 2: naive prefill on a 1024-token prefix (causal FLOPs scale as S^2)
+    S, Hq, Hkv, D = 1024, 32, 8, 128
+    q, k, v = bf16((S, Hq * D)), bf16((S, Hkv * D)), bf16((S, Hkv * D))
+    t = med(lambda: oracle.attention_prefill_naive(q, k, v, S, Hq, Hkv, D, fast=True))
+    fl = 4 * D * Hq * S * (S + 1) / 2
+    full = 4 * D * Hq * 2048 * 2049 / 2
+    res["config2_prefill"] = {"sample": "S=1024 prefix of config 2 (Hq=32 Hkv=8 D=128, causal, naive 3-pass)",
+                              "seconds": round(t, 4), "gflops": round(fl / t / 1e9, 2),
+                              "config2_seconds_at_that_rate": round(full / (fl / t), 3)}
+    # config 3: 16 sequential steps at B=32, H=16
+    B, H, d, T = 32, 16, 128, 16
+    x = [bf16((B, T, H, d)) for _ in range(3)]
+    a, b = bf16((B, T, H)), bf16((B, T, H))
+    S0 = rng.standard_normal((B, H, d, d), dtype=np.float32) * 0.02
+    t = med(lambda: oracle.deltanet_recurrent(x[0], x[1], x[2], a, b, S0, B, T, H, H, d, d, fast=True))
+    res["config3_deltanet_decode"] = {"sample": "16 sequential steps, B=32 H=16 dk=dv=128",
+                                      "us_per_step": round(t / T * 1e6, 1)}
+    # config 4: full sequence, sequential recurrence
+    T, Hk, Hv = 4096, 16, 32
+    x = [bf16((1, T, Hk, d)), bf16((1, T, Hk, d)), bf16((1, T, Hv, d))]
+    a, b = bf16((1, T, Hv)), bf16((1, T, Hv))
+    S0 = np.zeros((1, Hv, d, d), np.float32)
+    t = med(lambda: oracle.deltanet_recurrent(x[0], x[1], x[2], a, b, S0, 1, T, Hk, Hv, d, d, fast=True))
+    res["config4_deltanet_prefill"] = {"sample": "T=4096 Hk=16 Hv=32 dk=dv=128, sequential recurrence",
+                                       "seconds": round(t, 4), "tok_per_s": round(T / t)}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -648,7 +743,11 @@ def main():
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
         cpu = cpu_baseline(args.cpu_seconds)
+        cpu["cpu_model"] = cpu_model()
         log(f"[bench] CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        if not args.no_sub:
+            sub["cpu_baseline_configs"] = cpu_baseline_configs()
+            log(f"[bench] CPU baselines configs 2-4 {sub['cpu_baseline_configs']}")
     line = {
         "metric": METRIC,
         "value": round(value, 1),
