@@ -27,6 +27,8 @@ _SIGS = {
     "aila_hip_version": ([], _I),
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_gqa_decode_paged": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P], _I),
+    "aila_hip_kv_append_paged": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P], _I),
     "aila_hip_gqa_decode_noalloc_max_bytes": ([], _SZ),
     "aila_hip_gqa_decode_noalloc": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
@@ -144,6 +146,51 @@ def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
                                    int(cached_len), _ptr(seq_lens), _stream(stream))
     _check(rc, "aila_hip_gqa_decode")
     return out
+
+
+def gqa_decode_paged(q, k_pages, v_pages, block_table, seq_lens, max_len: int, out=None, workspace=None,
+                     stream=None):
+    """Decode over a paged cache. q [B,Hq,D]; k_pages/v_pages [num_pages,Hkv,
+    page_size,D] bf16; block_table int32 [B, max_pages]; seq_lens int32 [B]
+    (each <= max_len) -> out [B,Hq,D]."""
+    import torch
+    B, Hq, D = q.shape
+    num_pages, Hkv, page_size = k_pages.shape[0], k_pages.shape[1], k_pages.shape[2]
+    max_pages = block_table.shape[1]
+    _need(q, torch.bfloat16, (B, Hq, D), "q")
+    _need(k_pages, torch.bfloat16, (num_pages, Hkv, page_size, D), "k_pages")
+    _need(v_pages, torch.bfloat16, (num_pages, Hkv, page_size, D), "v_pages")
+    _need(block_table, torch.int32, (B, max_pages), "block_table", align=4)
+    _need(seq_lens, torch.int32, (B,), "seq_lens", align=4)
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.bfloat16, (B, Hq, D), "out")
+    ws_bytes = 0
+    if workspace is not None:
+        if not workspace.is_cuda or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous device tensor")
+        ws_bytes = workspace.numel() * workspace.element_size()
+    rc = lib().aila_hip_gqa_decode_paged(_ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(out), _ptr(workspace),
+                                         ws_bytes, B, Hq, Hkv, D, page_size, _ptr(block_table), max_pages,
+                                         int(max_len), _ptr(seq_lens), _stream(stream))
+    _check(rc, "aila_hip_gqa_decode_paged")
+    return out
+
+
+def kv_append_paged(k_new, v_new, k_pages, v_pages, block_table, positions, stream=None):
+    """k_new/v_new [B,Hkv,D] -> row positions[b] of sequence b in the page pool."""
+    import torch
+    num_pages, Hkv, page_size, D = k_pages.shape
+    B, max_pages = block_table.shape
+    _need(k_new, torch.bfloat16, (B, Hkv, D), "k_new")
+    _need(v_new, torch.bfloat16, (B, Hkv, D), "v_new")
+    _need(k_pages, torch.bfloat16, (num_pages, Hkv, page_size, D), "k_pages")
+    _need(v_pages, torch.bfloat16, (num_pages, Hkv, page_size, D), "v_pages")
+    _need(block_table, torch.int32, (B, max_pages), "block_table", align=4)
+    _need(positions, torch.int32, (B,), "positions", align=4)
+    rc = lib().aila_hip_kv_append_paged(_ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages), B, Hkv, D,
+                                        page_size, _ptr(block_table), max_pages, _ptr(positions), _stream(stream))
+    _check(rc, "aila_hip_kv_append_paged")
 
 
 def gqa_decode_noalloc(q, k_cache, v_cache, cached_len: int, out=None, seq_lens=None, stream=None):

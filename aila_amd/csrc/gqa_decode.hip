@@ -64,14 +64,25 @@ struct PrepArgs {
   float theta, eps;
 };
 
-template <int D, int G, bool PREP = false>
+// Paged KV cache: the rows of sequence b live in fixed-size pages of a
+// shared pool [num_pages, Hkv, page_size, D]; row t is row t % page_size of
+// page table[b * max_pages + t / page_size]. page_size is a multiple of the
+// 16-row chunk a wave loads, so a chunk never straddles two pages.
+struct PageArgs {
+  const int* table;      // [B, max_pages] device page indices
+  int page_size;
+  int max_pages;
+};
+
+template <int D, int G, bool PREP = false, bool PAGED = false>
 __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kc,
     const bf16* __restrict__ vc, bf16* __restrict__ out,
     float* __restrict__ part, int Hq, int Hkv, int max_seq, int L,
     const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max,
-    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new, PrepArgs pa) {
+    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new, PrepArgs pa, PageArgs pg) {
   static_assert(D % 32 == 0 && D <= 256, "D");
+  static_assert(!(PAGED && PREP), "the paged variant has no fused preparation");
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "G");
   constexpr int KS = D / 32;          // MFMA k-steps over the head dim
   constexpr int VL = D / 8;           // lanes per V row (16 B each)
@@ -92,10 +103,37 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m16 = lane & 15, g4 = lane >> 4;
-  const size_t kv_off = (static_cast<size_t>(b) * Hkv + kvh) * max_seq * D;
+  const size_t kv_off = PAGED ? 0 : (static_cast<size_t>(b) * Hkv + kvh) * max_seq * D;
   const bf16* K = kc + kv_off;
   const bf16* V = vc + kv_off;
   const int h0 = kvh * G;             // first query head of the group
+  // Element offset (from K / V) of cache row t0, the first row of a 16-row
+  // chunk; rows t0 .. t0 + 15 follow it contiguously in both layouts.
+  // `page` is the page holding t0 (paged layout only).
+  auto row_off = [&](int t0, int page) __attribute__((always_inline)) -> size_t {
+    if constexpr (PAGED) {
+      const int in_page = t0 - (t0 / pg.page_size) * pg.page_size;
+      return ((static_cast<size_t>(page) * Hkv + kvh) * pg.page_size + in_page) * D;
+    } else {
+      (void)page;
+      return static_cast<size_t>(t0) * D;
+    }
+  };
+  // page index of the chunk at t0 (uniform per wave). Branch-free: the
+  // table index is clamped to the sequence's row of the table, so a lookup
+  // for a chunk past the split reads a valid entry that is never used (an
+  // early return for such chunks, a branch on a wave-uniform value the
+  // compiler treats as divergent, measured wrong pages on gfx950).
+  auto page_of = [&](int t0) __attribute__((always_inline)) -> int {
+    if constexpr (PAGED) {
+      const int pi = min(t0 / pg.page_size, pg.max_pages - 1);
+      const int idx = __builtin_amdgcn_readfirstlane(b * pg.max_pages + pi);
+      return __builtin_amdgcn_readfirstlane(pg.table[idx]);
+    } else {
+      (void)t0;
+      return 0;
+    }
+  };
 
   __shared__ __attribute__((aligned(1024))) unsigned char s_k[kWaves][2][STAGE];
   __shared__ float s_p[kWaves][kChunk][G];
@@ -108,14 +146,15 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 
   // K rows of one 16-token chunk -> this wave's LDS stage, whole rows per
   // DMA instruction (lane order within a row follows the swizzle).
-  auto dma_k = [&](int stage, int t0) __attribute__((always_inline)) {
+  auto dma_k = [&](int stage, int t0, int page) __attribute__((always_inline)) {
     unsigned char* dst = s_k[wave][stage];
+    const bf16* Kc = K + row_off(t0, page);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int p = i * 64 + lane;
       const int r = p / NC, qc = (p % NC) ^ kswz<D>(r);
-      const int tok = min(t0 + r, s1 - 1);
-      __builtin_amdgcn_global_load_lds(K + static_cast<size_t>(tok) * D + qc * 8,
+      const int tok = min(t0 + r, s1 - 1) - t0;
+      __builtin_amdgcn_global_load_lds(Kc + static_cast<size_t>(tok) * D + qc * 8,
                                        (lds_void_t*)(dst + i * 1024), 16, 0, kNontemporal);
     }
   };
@@ -123,8 +162,9 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   // The first chunk's K DMA goes out before the query work whenever that
   // chunk cannot hold the row this launch appends (fused preparation).
   int t0 = s0 + wave * kChunk;
+  int pg_cur = page_of(t0);
   const bool early = PREP && t0 < s1 && t0 + kChunk <= len - 1;
-  if (early) dma_k(0, t0);
+  if (early) dma_k(0, t0, pg_cur);
 
   // Query operand (A rows = heads, zero rows for m16 >= G).
   bf16x8_t qa[KS];
@@ -248,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
       __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
     }
     __syncthreads();
-  } else if (k_new != nullptr && len > 0 && split == nsplit_b - 1) {
+  } else if (!PAGED && k_new != nullptr && len > 0 && split == nsplit_b - 1) {
     if (wave == 0 && lane < 2 * NC) {
       const int row = len - 1;
       const bool isv = lane >= NC;
@@ -261,7 +301,8 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     __syncthreads();
   }
 
-  if (!early && t0 < s1) dma_k(0, t0);
+  if (!early && t0 < s1) dma_k(0, t0, pg_cur);
+  int pg_nxt = page_of(t0 + kWaves * kChunk);
   for (int it = 0; t0 < s1; ++it, t0 += kWaves * kChunk) {
     const int stage = it & 1;
     // ---- K operands of this chunk (its DMA was issued one chunk earlier) --
@@ -273,13 +314,18 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     // ---- V rows of this chunk: nontemporal register loads, issued before
     //      the next K DMA so waiting on V never waits on that prefetch ------
     u32x4 vv[kChunk / VR];
+    const bf16* Vc = V + row_off(t0, pg_cur);
 #pragma unroll
     for (int i = 0; i < kChunk / VR; ++i) {
-      const int tok = min(t0 + vr + i * VR, s1 - 1);
-      vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(V + static_cast<size_t>(tok) * D + vd));
+      const int tok = min(t0 + vr + i * VR, s1 - 1) - t0;
+      vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Vc + static_cast<size_t>(tok) * D + vd));
     }
     const int t_next = t0 + kWaves * kChunk;
-    if (t_next < s1) dma_k(stage ^ 1, t_next);
+    if (t_next < s1) dma_k(stage ^ 1, t_next, pg_nxt);
+    // the page of the chunk after next goes out now, used one iteration later
+    const int pg_nn = page_of(t_next + kWaves * kChunk);
+    pg_cur = pg_nxt;
+    pg_nxt = pg_nn;
     // ---- scores on MFMA ------------------------------------------------------
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -514,6 +560,7 @@ struct DecodeArgs {
   const bf16* k_new;     // fused append (null: none)
   const bf16* v_new;
   PrepArgs prep;         // q_stride = 0: no fused preparation
+  PageArgs pages;        // table = null: contiguous [B, Hkv, max_seq, D] cache
 };
 
 template <int D, int G>
@@ -522,11 +569,15 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
   if (a.prep.q_stride > 0)
     hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep);
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
+  else if (a.pages.table != nullptr)
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0,
+                       st, a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
   else
     hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep);
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
   if (a.part) {
     hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
                        a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit_max);
@@ -591,7 +642,7 @@ int dispatch_g(int G, const DecodeArgs& a, hipStream_t st) {
 int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, void* workspace,
                     size_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_seq, int cached_len,
                     const int* seq_lens, int len_bias, const void* k_new, const void* v_new,
-                    hipStream_t st, const PrepArgs* prep = nullptr) {
+                    hipStream_t st, const PrepArgs* prep = nullptr, const PageArgs* pages = nullptr) {
   AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
   AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
                "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
@@ -607,6 +658,7 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
   a.k_new = static_cast<const bf16*>(k_new);
   a.v_new = static_cast<const bf16*>(v_new);
   a.prep = prep ? *prep : PrepArgs{};
+  a.pages = pages ? *pages : PageArgs{};
   // Records per (sequence, head) that the workspace holds; the split count
   // adapts to it (the reference's [Hq, max_tiles, 272] partials buffer for
   // D=256 is accepted as-is).
@@ -654,6 +706,24 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache, const voi
                                    int max_seq, int cached_len, const int* seq_lens, void* stream) {
   return aila::gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq,
                                cached_len, seq_lens, 0, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aila_hip_gqa_decode_paged(const void* q, const void* k_pages, const void* v_pages, void* out,
+                                         void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int D,
+                                         int page_size, const int* block_table, int max_pages, int max_len,
+                                         const int* seq_lens, void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(block_table && seq_lens, "gqa_decode_paged: block_table and seq_lens are required");
+  AILA_REQUIRE(page_size > 0 && page_size % kChunk == 0,
+               "gqa_decode_paged: page_size=%d must be a positive multiple of %d", page_size, kChunk);
+  AILA_REQUIRE(max_pages > 0 && static_cast<long>(max_pages) * page_size <= (1L << 30),
+               "gqa_decode_paged: bad max_pages=%d", max_pages);
+  const int max_seq = max_pages * page_size;
+  AILA_REQUIRE(max_len >= 0 && max_len <= max_seq, "gqa_decode_paged: max_len=%d outside [0, %d]", max_len,
+               max_seq);
+  PageArgs pg{block_table, page_size, max_pages};
+  return gqa_decode_impl(q, k_pages, v_pages, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, max_len,
+                         seq_lens, 0, nullptr, nullptr, static_cast<hipStream_t>(stream), nullptr, &pg);
 }
 
 // ---------------------------------------------------------------------------
@@ -794,4 +864,44 @@ extern "C" int aila_hip_kv_append(const void* k_new, const void* v_new, void* k_
                      static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache), B, Hkv, D, max_seq, pos,
                      positions);
   return check_launch("kv_append");
+}
+
+namespace aila {
+namespace {
+// One new token per sequence into its page: row positions[b] of sequence b
+// is row positions[b] % page_size of page table[b * max_pages +
+// positions[b] / page_size]. One 16-byte chunk per thread.
+__global__ void kv_append_paged_kernel(const u32x4* __restrict__ kn, const u32x4* __restrict__ vn,
+                                       bf16* __restrict__ kp, bf16* __restrict__ vp, int B, int Hkv, int D,
+                                       int page_size, const int* __restrict__ table, int max_pages,
+                                       const int* __restrict__ positions) {
+  const int chunks = D / 8;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * Hkv * chunks) return;
+  const int b = i / (Hkv * chunks);
+  const int h = (i / chunks) % Hkv;
+  const int c = i % chunks;
+  const int p = positions[b];
+  if (p < 0 || p >= max_pages * page_size) return;
+  const int page = table[b * max_pages + p / page_size];
+  const size_t dst = ((static_cast<size_t>(page) * Hkv + h) * page_size + p % page_size) * D + c * 8;
+  *reinterpret_cast<u32x4*>(kp + dst) = kn[i];
+  *reinterpret_cast<u32x4*>(vp + dst) = vn[i];
+}
+}  // namespace
+}  // namespace aila
+
+extern "C" int aila_hip_kv_append_paged(const void* k_new, const void* v_new, void* k_pages, void* v_pages, int B,
+                                        int Hkv, int D, int page_size, const int* block_table, int max_pages,
+                                        const int* positions, void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(k_new && v_new && k_pages && v_pages && block_table && positions, "kv_append_paged: null pointer");
+  AILA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D % 8 == 0 && page_size > 0 && max_pages > 0,
+               "kv_append_paged: bad shape (B=%d Hkv=%d D=%d page_size=%d max_pages=%d)", B, Hkv, D, page_size,
+               max_pages);
+  const int n = B * Hkv * (D / 8);
+  hipLaunchKernelGGL(kv_append_paged_kernel, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(k_new), static_cast<const u32x4*>(v_new), static_cast<bf16*>(k_pages),
+                     static_cast<bf16*>(v_pages), B, Hkv, D, page_size, block_table, max_pages, positions);
+  return check_launch("kv_append_paged");
 }

@@ -65,6 +65,38 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int B, int Hq, int Hkv, int D, int max_seq,
                         int cached_len, const int* seq_lens, void* stream);
 
+/* GQA decode over a paged KV cache. The reference keeps one contiguous
+ * [Hkv, max_seq, D] cache per sequence (src/memory/KVCache.hpp:9-45) and
+ * has no paged layout; this is the paged option of the same decode
+ * (ops::attention_decode, src/ops/AttentionOps.cpp:499-643) for serving
+ * engines that allocate the cache in fixed-size pages.
+ *   k_pages, v_pages  [num_pages, Hkv, page_size, D] bf16 page pool
+ *   block_table       device int[B, max_pages]: row t of sequence b is row
+ *                     t % page_size of page block_table[b*max_pages + t/page_size]
+ *   seq_lens          device int[B] (required): sequence b attends rows
+ *                     [0, min(seq_lens[b], max_len))
+ *   max_len           host bound on every seq_lens[b] (<= max_pages*page_size);
+ *                     it sizes the split plan as cached_len does.
+ *   page_size         a multiple of 16.
+ * Other arguments, the workspace and the results as aila_hip_gqa_decode
+ * (identical results for identical rows). */
+int aila_hip_gqa_decode_paged(const void* q, const void* k_pages,
+                              const void* v_pages, void* out, void* workspace,
+                              size_t workspace_bytes, int B, int Hq, int Hkv,
+                              int D, int page_size, const int* block_table,
+                              int max_pages, int max_len, const int* seq_lens,
+                              void* stream);
+
+/* Append one token's K/V row per sequence into its page: k_new/v_new
+ * [B, Hkv, D] bf16 go to row positions[b] (device int[B]) of sequence b in
+ * the paged layout of aila_hip_gqa_decode_paged. Positions outside
+ * [0, max_pages*page_size) are skipped. (The paged counterpart of the cache
+ * write of ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:105-216.) */
+int aila_hip_kv_append_paged(const void* k_new, const void* v_new,
+                             void* k_pages, void* v_pages, int B, int Hkv,
+                             int D, int page_size, const int* block_table,
+                             int max_pages, const int* positions, void* stream);
+
 /* Allocation-free variant of aila_hip_gqa_decode. No counterpart in the
  * reference: it is for callers that cannot allocate device memory or pass a
  * workspace (code under HIP graph capture, tight serving loops, harnesses
