@@ -45,7 +45,7 @@ _SIGS = {
     "aila_hip_deltanet_layer_prefill": ([_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _SZ,
                                          _I, _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
     "aila_hip_deltanet_layer_decode": ([_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P,
-                                        _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
+                                        _I, _I, _I, _I, _I, _I, _F, _F, _P, _P], _I),
     "aila_hip_decode_prepare_qkv": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                                      _I, _I, _I, _I, _I, _I, _F, _F, _I, _P, _P], _I),
     "aila_hip_head_rms_norm": ([_P, _P, _I, _I, _I, _F, _P], _I),
@@ -361,7 +361,7 @@ def _rows(t, dtype, B, width, name, align=2):
 
 def deltanet_layer_decode(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, state, num_k_heads,
                           out=None, conv_heads=None, dt_bias=None, A_log=None, eps: float = 1e-6,
-                          scale: float | None = None, stream=None):
+                          scale: float | None = None, arrivals=None, stream=None):
     """Full Gated DeltaNet layer step for B sequences: conv1d ring (+SiLU),
     L2 norm, gated delta recurrence, RMSNorm(o) * norm_w * SiLU(z).
 
@@ -369,7 +369,9 @@ def deltanet_layer_decode(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, s
     strided views); conv_w [ch, 4] bf16; conv_state [B, 3, ch] fp32 and
     state [B, Hv, dk, dv] fp32 are updated in place; conv_head (int) or
     conv_heads (int32 [B], device) gives the ring row of the oldest input.
-    Returns out [B, Hv*dv] bf16."""
+    ``arrivals``: optional int32 [B*Hk] device tensor, zero before the first
+    call (every call leaves it zero): one workgroup per value head instead
+    of one per key head. Returns out [B, Hv*dv] bf16."""
     import torch
     B, Hv, dk, dv = state.shape
     Hk = int(num_k_heads)
@@ -396,10 +398,12 @@ def deltanet_layer_decode(qkv, z, a, b, conv_w, conv_state, conv_head, norm_w, s
     _need(out, torch.bfloat16, (B, Hv * dv), "out", align=8)
     if scale is None:
         scale = 1.0 / math.sqrt(dk)
+    if arrivals is not None:
+        _need(arrivals, torch.int32, (B * Hk,), "arrivals", align=4)
     rc = lib().aila_hip_deltanet_layer_decode(
         _ptr(qkv), qs, _ptr(z), zs, _ptr(a), _ptr(b), ast, _ptr(conv_w), _ptr(conv_state), int(conv_head),
         _ptr(conv_heads), _ptr(dt_bias), _ptr(A_log), _ptr(norm_w), _ptr(state), _ptr(out), B, Hk, Hv, dk, dv,
-        K, float(eps), float(scale), _stream(stream))
+        K, float(eps), float(scale), _ptr(arrivals), _stream(stream))
     _check(rc, "aila_hip_deltanet_layer_decode")
     return out
 

@@ -191,6 +191,178 @@ __global__ __launch_bounds__(256 * G) void deltanet_layer_decode_kernel(
   }
 }
 
+// One workgroup of 256 threads per (value head, sequence): twice (G = 2) or
+// four times (G = 4) the workgroups of the kernel above, for batches that
+// leave CUs idle with one workgroup per key head. The G workgroups of a key
+// head all read the q/k ring rows of that key head; the one that arrives
+// last - after every other has finished reading them, counted with one
+// device-scope atomic per (sequence, key head) in the caller's `arrivals`
+// array - writes the new q/k raw row there and resets the count to zero.
+// Each workgroup writes the ring entries of its own v channels.
+template <int G, int NT>
+__global__ __launch_bounds__(NT) void deltanet_layer_decode_vh_kernel(
+    const bf16* __restrict__ qkv, int qkv_stride, const bf16* __restrict__ z, int z_stride,
+    const bf16* __restrict__ a, const bf16* __restrict__ bgate, int ab_stride,
+    const bf16* __restrict__ conv_w, float* __restrict__ conv_state, int conv_head,
+    const int* __restrict__ conv_heads, const bf16* __restrict__ dt_bias, const float* __restrict__ A_log,
+    const float* __restrict__ norm_w, float* __restrict__ state, bf16* __restrict__ out, int Hk, float eps,
+    float scale, unsigned int* __restrict__ arrivals) {
+  const int hv = blockIdx.x, bseq = blockIdx.y;
+  const int hk = hv / G;
+  const int Hv = Hk * G;
+  const int qd = Hk * kD, ch = 2 * qd + Hv * kD;
+  constexpr int NW = NT / 64;                   // waves
+  constexpr int RPT = kD / (NT / kColQuads);    // state rows per thread
+  const int t = threadIdx.x;
+  const int cq = t % kColQuads, rg = t / kColQuads;
+  const int col = cq * 4;
+  const int lane = t & 63, wave = t >> 6;
+
+  __shared__ float s_act[3 * kD];               // conv+SiLU outputs: q, k, v
+  __shared__ float s_red[2][NW][kColQuads * 4];
+  __shared__ int s_last;
+
+  float* S = state + (static_cast<size_t>(bseq) * Hv + hv) * kD * kD;
+
+  // 1. conv inputs of q, k (key head hk) and v (value head hv), gates, then
+  //    the state slab (the convolution waits only for its own loads)
+  constexpr int kCh = 3 * kD;
+  constexpr int kCPT = (kCh + NT - 1) / NT;
+  int head = conv_heads ? conv_heads[bseq] : conv_head;
+  head = ((head % kRows) + kRows) % kRows;
+  const int head1 = head == kRows - 1 ? 0 : head + 1;
+  const int head2 = head == 0 ? kRows - 1 : head - 1;
+  const bf16* x = qkv + static_cast<size_t>(bseq) * qkv_stride;
+  float* ring = conv_state + static_cast<size_t>(bseq) * kRows * ch;
+  int cidx[kCPT];
+  uint2 wr[kCPT];
+  float xv[kCPT], h0[kCPT], h1[kCPT], h2[kCPT];
+#pragma unroll
+  for (int i = 0; i < kCPT; ++i) {
+    const int lc = t + i * NT;
+    const int lcc = lc < kCh ? lc : kCh - 1;
+    const int c = lcc < kD ? hk * kD + lcc : (lcc < 2 * kD ? qd + hk * kD + lcc - kD : 2 * qd + hv * kD + lcc - 2 * kD);
+    cidx[i] = c;
+    wr[i] = *reinterpret_cast<const uint2*>(conv_w + static_cast<size_t>(c) * kConvK);
+    xv[i] = bf2f(x[c]);
+    h0[i] = ring[static_cast<size_t>(head) * ch + c];
+    h1[i] = ring[static_cast<size_t>(head1) * ch + c];
+    h2[i] = ring[static_cast<size_t>(head2) * ch + c];
+  }
+  const size_t ai = static_cast<size_t>(bseq) * ab_stride + hv;
+  const float b_raw = bf2f(bgate[ai]);
+  const float a_raw = bf2f(a[ai]);
+  const float dtb = dt_bias ? bf2f(dt_bias[hv]) : 0.0f;
+  const float alog = A_log ? A_log[hv] : 0.0f;
+  const f32x4 nw = *reinterpret_cast<const f32x4*>(norm_w + col);
+  const uint2 zr = *reinterpret_cast<const uint2*>(z + static_cast<size_t>(bseq) * z_stride + hv * kD + col);
+
+  f32x4 s[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r)
+    s[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + static_cast<size_t>(rg * RPT + r) * kD + col));
+
+  // 2. conv + SiLU into LDS; own v channels' ring entries replaced now
+#pragma unroll
+  for (int i = 0; i < kCPT; ++i) {
+    const int lc = t + i * NT;
+    if (lc < kCh) {
+      float acc = h0[i] * __uint_as_float(wr[i].x << 16);
+      acc += h1[i] * __uint_as_float(wr[i].x & 0xffff0000u);
+      acc += h2[i] * __uint_as_float(wr[i].y << 16);
+      acc += xv[i] * __uint_as_float(wr[i].y & 0xffff0000u);
+      s_act[lc] = silu_f(acc);
+      if (lc >= 2 * kD) ring[static_cast<size_t>(head) * ch + cidx[i]] = xv[i];
+    }
+  }
+  const float beta = 1.0f / (1.0f + expf(-b_raw));
+  const float negA = A_log ? -expf(alog) : -1.0f;
+  const float decay = expf(softplus_f(a_raw + dtb) * negA);
+  __syncthreads();
+  // Every thread's ring reads are complete (their values were used above):
+  // count this workgroup's arrival for the key head.
+  unsigned int* cnt = arrivals + static_cast<size_t>(bseq) * Hk + hk;
+  unsigned int arrived = 0;
+  if (t == 0) arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // 3. L2 norms of q and k
+  float sq = s_act[lane] * s_act[lane] + s_act[lane + 64] * s_act[lane + 64];
+  float sk = s_act[kD + lane] * s_act[kD + lane] + s_act[kD + lane + 64] * s_act[kD + lane + 64];
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  const float qn = 1.0f / sqrtf(sq + eps);
+  const float kn = 1.0f / sqrtf(sk + eps);
+
+  // 4. S *= decay; u = S^T k
+  float kr[RPT];
+  f32x4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    kr[r] = s_act[kD + rg * RPT + r] * kn;
+    s[r] *= decay;
+    u += s[r] * kr[r];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) u[e] += __shfl_xor(u[e], 32);
+  if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[0][wave][cq * 4]) = u;
+  if (t == 0) {
+    const bool last = arrived == static_cast<unsigned int>(G - 1);
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  u = *reinterpret_cast<const f32x4*>(&s_red[0][0][cq * 4]);
+#pragma unroll
+  for (int w = 1; w < NW; ++w) u += *reinterpret_cast<const f32x4*>(&s_red[0][w][cq * 4]);
+  // the last of the key head's workgroups replaces the q/k ring row
+  if (s_last) {
+#pragma unroll
+    for (int i = 0; i < kCPT; ++i) {
+      const int lc = t + i * NT;
+      if (lc < 2 * kD) ring[static_cast<size_t>(head) * ch + cidx[i]] = xv[i];
+    }
+  }
+
+  // 5. d = (v - u) beta; S += k d^T; o = S^T q; one write of the state
+  const f32x4 vv = *reinterpret_cast<const f32x4*>(&s_act[2 * kD + col]);
+  const f32x4 d = (vv - u) * beta;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const float qr = s_act[rg * RPT + r] * qn;
+    s[r] += kr[r] * d;
+    o += s[r] * qr;
+  }
+#pragma unroll
+  for (int r = 0; r < RPT; ++r)
+    __builtin_nontemporal_store(s[r], reinterpret_cast<f32x4*>(S + static_cast<size_t>(rg * RPT + r) * kD + col));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] += __shfl_xor(o[e], 32);
+  if (lane < 32) *reinterpret_cast<f32x4*>(&s_red[1][wave][cq * 4]) = o;
+  __syncthreads();
+
+  // 6. output gate: RMSNorm over the 128 outputs * norm_w * SiLU(z)
+  if (t < kColQuads) {
+    o = *reinterpret_cast<const f32x4*>(&s_red[1][0][cq * 4]);
+#pragma unroll
+    for (int w = 1; w < NW; ++w) o += *reinterpret_cast<const f32x4*>(&s_red[1][w][cq * 4]);
+    o *= scale;
+    float ss = o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3];
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+    const float zf[4] = {__uint_as_float(zr.x << 16), __uint_as_float(zr.x & 0xffff0000u),
+                         __uint_as_float(zr.y << 16), __uint_as_float(zr.y & 0xffff0000u)};
+    float r4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r4[e] = o[e] * inv * nw[e] * silu_f(zf[e]);
+    uint2 w;
+    w.x = pack_bf16x2(r4[0], r4[1]);
+    w.y = pack_bf16x2(r4[2], r4[3]);
+    *reinterpret_cast<uint2*>(out + (static_cast<size_t>(bseq) * Hv + hv) * kD + col) = w;
+  }
+}
+
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
 // ---- prefill: causal conv + SiLU over T tokens into split planes ----------
@@ -461,7 +633,8 @@ extern "C" int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride, c
                                               float* conv_state, int conv_head, const int* conv_heads,
                                               const void* dt_bias, const float* A_log, const float* norm_w,
                                               float* state, void* out, int B, int Hk, int Hv, int dk, int dv,
-                                              int conv_kernel, float eps, float scale, void* stream) {
+                                              int conv_kernel, float eps, float scale, unsigned int* arrivals,
+                                              void* stream) {
   using namespace aila;
   AILA_REQUIRE(qkv && z && a && b && conv_w && conv_state && norm_w && state && out,
                "deltanet_layer_decode: null pointer");
@@ -475,8 +648,8 @@ extern "C" int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride, c
                "deltanet_layer_decode: row strides too small (qkv %d < %d, z %d, ab %d)", qkv_stride, ch,
                z_stride, ab_stride);
   AILA_REQUIRE(aligned(conv_w, 8) && aligned(z, 8) && z_stride % 4 == 0 && aligned(norm_w, 16) &&
-                   aligned(state, 16) && aligned(out, 8),
-               "deltanet_layer_decode: misaligned conv_w/z/norm_w/state/out");
+                   aligned(state, 16) && aligned(out, 8) && aligned(arrivals, 4),
+               "deltanet_layer_decode: misaligned conv_w/z/norm_w/state/out/arrivals");
   const int G = Hv / Hk;
   const dim3 grid(Hk, B);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -491,13 +664,29 @@ extern "C" int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride, c
   hipLaunchKernelGGL(deltanet_layer_decode_kernel<GG>, grid, dim3(256 * GG), 0, st, qp, qkv_stride, zp,    \
                      z_stride, ap, bp, ab_stride, wp, conv_state, conv_head, conv_heads, dtp, A_log, norm_w, \
                      state, op, Hk, eps, scale)
-  switch (G) {
-    case 1: AILA_LAYER_DECODE(1); break;
-    case 2: AILA_LAYER_DECODE(2); break;
-    case 4: AILA_LAYER_DECODE(4); break;
-    default:
-      return set_error(AILA_HIP_EUNSUPPORTED, "deltanet_layer_decode: Hv/Hk = %d not in {1,2,4}", G);
+#define AILA_LAYER_DECODE_VH(GG)                                                                           \
+  hipLaunchKernelGGL((deltanet_layer_decode_vh_kernel<GG, 256>), dim3(Hv, B), dim3(256), 0, st, qp, qkv_stride, zp, \
+                     z_stride, ap, bp, ab_stride, wp, conv_state, conv_head, conv_heads, dtp, A_log, norm_w,  \
+                     state, op, Hk, eps, scale, arrivals)
+  // With an arrivals array and G > 1, one workgroup per value head (more
+  // workgroups in flight); otherwise one per key head.
+  if (arrivals != nullptr && G > 1) {
+    switch (G) {
+      case 2: AILA_LAYER_DECODE_VH(2); break;
+      case 4: AILA_LAYER_DECODE_VH(4); break;
+      default:
+        return set_error(AILA_HIP_EUNSUPPORTED, "deltanet_layer_decode: Hv/Hk = %d not in {1,2,4}", G);
+    }
+  } else {
+    switch (G) {
+      case 1: AILA_LAYER_DECODE(1); break;
+      case 2: AILA_LAYER_DECODE(2); break;
+      case 4: AILA_LAYER_DECODE(4); break;
+      default:
+        return set_error(AILA_HIP_EUNSUPPORTED, "deltanet_layer_decode: Hv/Hk = %d not in {1,2,4}", G);
+    }
   }
 #undef AILA_LAYER_DECODE
+#undef AILA_LAYER_DECODE_VH
   return check_launch("deltanet_layer_decode");
 }

@@ -139,11 +139,14 @@ void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Ten
 // (LayerCache::linear_conv_state / linear_state) updated in place;
 // norm_weight [dv] fp32; out [1, Hv*dv] bf16. conv_head is the cache's
 // linear_conv_head and is advanced by one, as the backend does (:1163).
-// scale = 1/sqrt(head_k_dim) as in the backend (:991).
+// scale = 1/sqrt(head_k_dim) as in the backend (:991). arrivals (s32
+// [num_k_heads], zeroed once, left zero by every call) lets the layer run
+// one workgroup per value head; null runs one per key head.
 void linear_delta_layer_decode(Context& ctx, Tensor& qkv, Tensor& z, Tensor& a, Tensor& b, Tensor& conv1d_weight,
                                Tensor& conv_state, int& conv_head, Tensor* dt_bias, Tensor* A_log,
                                Tensor& norm_weight, Tensor& state, Tensor& out, int num_k_heads, int num_v_heads,
-                               int head_k_dim, int head_v_dim, int conv_kernel, float eps);
+                               int head_k_dim, int head_v_dim, int conv_kernel, float eps,
+                               Tensor* arrivals = nullptr);
 
 // run_linear_delta_prefill_gpu_batched (:1306-1508): fused_all [seq_len,
 // all_dim] rows of [qkv | z | a | b] (all_dim = conv_ch + Hv*dv + 2*Hv),

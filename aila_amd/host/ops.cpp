@@ -231,8 +231,9 @@ void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Ten
 void linear_delta_layer_decode(Context& ctx, Tensor& qkv, Tensor& z, Tensor& a, Tensor& b, Tensor& conv1d_weight,
                                Tensor& conv_state, int& conv_head, Tensor* dt_bias, Tensor* A_log,
                                Tensor& norm_weight, Tensor& state, Tensor& out, int num_k_heads, int num_v_heads,
-                               int head_k_dim, int head_v_dim, int conv_kernel, float eps) {
+                               int head_k_dim, int head_v_dim, int conv_kernel, float eps, Tensor* arrivals) {
   for (Tensor* t : {&qkv, &z, &a, &b, &conv1d_weight, &out}) need_dtype(*t, DType::bf16, "linear_delta_layer_decode");
+  if (arrivals) need_dtype(*arrivals, DType::s32, "linear_delta_layer_decode arrivals");
   for (Tensor* t : {&conv_state, &state, &norm_weight}) need_dtype(*t, DType::f32, "linear_delta_layer_decode");
   const int ch = 2 * num_k_heads * head_k_dim + num_v_heads * head_v_dim;
   const float scale = 1.0f / std::sqrt(static_cast<float>(head_k_dim));
@@ -241,7 +242,8 @@ void linear_delta_layer_decode(Context& ctx, Tensor& qkv, Tensor& z, Tensor& a, 
                                        nullptr, dt_bias ? dt_bias->data() : nullptr,
                                        A_log ? A_log->data_as<float>() : nullptr, norm_weight.data_as<float>(),
                                        state.data_as<float>(), out.data(), 1, num_k_heads, num_v_heads, head_k_dim,
-                                       head_v_dim, conv_kernel, eps, scale, ctx.stream()),
+                                       head_v_dim, conv_kernel, eps, scale,
+                                       arrivals ? static_cast<unsigned int*>(arrivals->data()) : nullptr, ctx.stream()),
         "linear_delta_layer_decode");
   if (conv_kernel > 1) conv_head = (conv_head + 1) % (conv_kernel - 1);
 }

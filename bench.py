@@ -343,8 +343,11 @@ def sub_deltanet_layer_decode(torch, aila_amd, steps=512, per_graph=16):
           for _ in range(per_graph)]
     out = torch.empty((B, Hv * d), **bf)
     heads = torch.zeros((B,), dtype=torch.int32, device="cuda")
+    # arrival counts (zeroed once, left zero by every call): one workgroup per
+    # value head
+    arr = torch.zeros((B * Hk,), dtype=torch.int32, device="cuda")
     fn = lambda x: aila_amd.deltanet_layer_decode(x["qkv"], x["z"], x["a"], x["b"], w, cs, 0, nw, st, Hk,
-                                                  out=out, conv_heads=heads)
+                                                  out=out, conv_heads=heads, arrivals=arr)
     for x in xs:
         fn(x)
     torch.cuda.synchronize()
@@ -378,7 +381,7 @@ def sub_deltanet_layer_decode(torch, aila_amd, steps=512, per_graph=16):
     with torch.cuda.graph(gr3):
         for i in range(nl):
             aila_amd.deltanet_layer_decode(x0["qkv"], x0["z"], x0["a"], x0["b"], w, css[i], 0, nw, sts[i], Hk,
-                                           out=out, conv_heads=heads)
+                                           out=out, conv_heads=heads, arrivals=arr)
     with torch.cuda.graph(gr4):
         for i in range(nl):
             aila_amd.deltanet_decode(q[0], q[1], v, x0["a"], x0["b"], sts[i], out=o2)

@@ -235,7 +235,14 @@ int aila_hip_deltanet_decode(const void* q, const void* k, const void* v,
  *         z row b at z + b*z_stride, norm_w [dv] fp32 (:1153-1160, :153-173).
  * state [B, Hv, dk, dv] fp32 is read and written once. Supported: dk = dv =
  * 128, conv kernel 4, Hv / Hk in {1, 2, 4} (the reference fast path's
- * shapes). */
+ * shapes).
+ *   arrivals  optional device uint32[B*Hk], zero before the first call and
+ *             left zero by every call: with it (and Hv > Hk) the layer runs
+ *             one workgroup per value head instead of one per key head (the
+ *             key head's workgroups count their reads of the shared q/k ring
+ *             row in it, and the last one replaces that row). Calls that
+ *             overlap in time must not share one array. NULL: one workgroup
+ *             per key head. Same results either way. */
 int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride,
                                    const void* z, int z_stride, const void* a,
                                    const void* b, int ab_stride,
@@ -245,7 +252,8 @@ int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride,
                                    const float* norm_w, float* state,
                                    void* out, int B, int Hk, int Hv, int dk,
                                    int dv, int conv_kernel, float eps,
-                                   float scale, void* stream);
+                                   float scale, unsigned int* arrivals,
+                                   void* stream);
 
 /* Workspace bytes for aila_hip_deltanet_layer_prefill: the split conv
  * outputs (q; k and v as bf16 hi + bf16 residual planes) and the chunk

@@ -60,28 +60,51 @@ def _oracle(x, B, T, Hk, Hv, head):
                                  A_log=x["A_log"], fast=True)
 
 
-@pytest.mark.parametrize("B,Hk,Hv,T,head0", [(3, 2, 4, 24, 0), (2, 3, 3, 10, 2), (1, 1, 4, 10, 1),
-                                             (8, 16, 32, 6, 0)])
-def test_layer_decode_steps_match_oracle(B, Hk, Hv, T, head0):
+def _run_layer_steps(x, B, T, Hk, head0, wide):
+    """T decode steps; wide: one workgroup per value head (arrivals array).
+    Returns (out bf16 bits [B, T, Hv*dv], state, conv ring, arrivals)."""
     import torch
     import aila_amd
-    x = _inputs(900 + Hv, B, T, Hk, Hv)
-    want_out, want_S, want_cs = _oracle(x, B, T, Hk, Hv, head0)
     st, cs = _t(x["state"]), _t(x["conv_state"])
     w, nw, dtb, alog = _t(x["conv_w"]), _t(x["norm_w"]), _t(x["dt_bias"]), _t(x["A_log"])
     qkv, z, a, b = _t(x["qkv"]), _t(x["z"]), _t(x["a"]), _t(x["b"])
+    arr = torch.zeros(B * Hk, dtype=torch.int32, device="cuda") if wide else None
     outs = []
     for t in range(T):
         o = aila_amd.deltanet_layer_decode(qkv[:, t], z[:, t], a[:, t], b[:, t], w, cs, (head0 + t) % 3, nw, st,
-                                           Hk, dt_bias=dtb, A_log=alog)
+                                           Hk, dt_bias=dtb, A_log=alog, arrivals=arr)
         outs.append(o)
     torch.cuda.synchronize()
-    got = np.stack([_np(o) for o in outs], axis=1)
-    e_s = _rel(_np(st), want_S)
+    return (np.stack([_np(o) for o in outs], axis=1), _np(st), _np(cs),
+            arr.cpu().numpy() if wide else None)
+
+
+@pytest.mark.parametrize("wide", [False, True])
+@pytest.mark.parametrize("B,Hk,Hv,T,head0", [(3, 2, 4, 24, 0), (2, 3, 3, 10, 2), (1, 1, 4, 10, 1),
+                                             (8, 16, 32, 6, 0)])
+def test_layer_decode_steps_match_oracle(B, Hk, Hv, T, head0, wide):
+    x = _inputs(900 + Hv, B, T, Hk, Hv)
+    want_out, want_S, want_cs = _oracle(x, B, T, Hk, Hv, head0)
+    got, got_S, got_cs, arr = _run_layer_steps(x, B, T, Hk, head0, wide)
+    e_s = _rel(got_S, want_S)
     e_o = _rel(dg.bf16_to_f32(got), dg.bf16_to_f32(want_out))
     assert e_s <= STATE_TOL, f"state relerr {e_s}"
     assert e_o <= OUT_TOL, f"out relerr {e_o}"
-    assert np.array_equal(_np(cs), want_cs), "conv ring must hold the raw inputs bit-exact"
+    assert np.array_equal(got_cs, want_cs), "conv ring must hold the raw inputs bit-exact"
+    if wide:
+        assert not arr.any(), "every call leaves the arrival counts at zero"
+
+
+@pytest.mark.parametrize("B,Hk,Hv", [(8, 16, 32), (3, 2, 8 // 2 * 2), (2, 1, 4)])
+def test_layer_decode_wide_equals_narrow(B, Hk, Hv):
+    """One workgroup per value head (shared q/k ring row replaced by the
+    last arriving workgroup) gives the same bits as one per key head."""
+    T = 12
+    x = _inputs(977 + B, B, T, Hk, Hv)
+    n_out, n_S, n_cs, _ = _run_layer_steps(x, B, T, Hk, 1, False)
+    w_out, w_S, w_cs, arr = _run_layer_steps(x, B, T, Hk, 1, True)
+    assert np.array_equal(n_out, w_out) and np.array_equal(n_S.view(np.uint32), w_S.view(np.uint32))
+    assert np.array_equal(n_cs, w_cs) and not arr.any()
 
 
 def test_layer_decode_fused_rows_and_device_heads():
