@@ -375,7 +375,7 @@ bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) %
 // activation to 2^-16 relative. The first token block also writes the new
 // ring (the last three raw rows, oldest at row (head + T) % 3): it is the
 // only block that reads or writes the ring.
-constexpr int kConvTok = 16;
+constexpr int kConvTok = 16;    // (32 and 64 measured 1-3% slower at the config-4 shape)
 constexpr int kConvBatch = 8;   // rows loaded together before they are used
 
 template <int CPT>
@@ -427,58 +427,67 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
         w[i][j] = __uint_as_float(((i * 4 + j) & 1) ? (word & 0xffff0000u) : (word << 16));
       }
   }
-  struct Row { float v[CPT]; };
-  auto load_x = [&](int t) __attribute__((always_inline)) {
-    Row r;
-    unpack_bf16<CPT>(*reinterpret_cast<const Raw*>(xb + static_cast<size_t>(t) * qkv_stride), r.v);
-    return r;
+  // All per-row values live in plain float arrays indexed by compile-time
+  // constants (a runtime choice among local rows puts them in scratch).
+  auto load_x = [&](int t, float (&dst)[CPT]) __attribute__((always_inline)) {
+    unpack_bf16<CPT>(*reinterpret_cast<const Raw*>(xb + static_cast<size_t>(t) * qkv_stride), dst);
   };
-  Row old_ring[kRows];
-  auto hist = [&](int i) __attribute__((always_inline)) {   // raw row i (i >= -3)
-    return i < 0 ? old_ring[i + kRows] : load_x(i);
-  };
-  if (tb0 == 0) {
-#pragma unroll
-    for (int j = 0; j < kRows; ++j)
+  // raw row i (i >= -3) into dst: token rows from qkv, i < 0 from the ring
+  // (ring row (head + 3 + i) % 3 holds raw row i)
+  auto hist = [&](int i, float (&dst)[CPT]) __attribute__((always_inline)) {
+    if (i >= 0) {
+      load_x(i, dst);
+    } else {
 #pragma unroll
       for (int v4 = 0; v4 < CPT / 4; ++v4) {
-        const f32x4 r = *reinterpret_cast<const f32x4*>(ring + static_cast<size_t>((head + j) % kRows) * ch + v4 * 4);
+        const f32x4 r = *reinterpret_cast<const f32x4*>(ring + static_cast<size_t>((head + kRows + i) % kRows) * ch + v4 * 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) old_ring[j].v[v4 * 4 + e] = r[e];
+        for (int e = 0; e < 4; ++e) dst[v4 * 4 + e] = r[e];
       }
-  }
-  Row h0 = hist(tb0 - 3), h1 = hist(tb0 - 2), h2 = hist(tb0 - 1);
+    }
+  };
+  float h0[CPT], h1[CPT], h2[CPT];
+  hist(tb0 - 3, h0);
+  hist(tb0 - 2, h1);
+  hist(tb0 - 1, h2);
   // destination plane and column
   const bool is_q = c < qd, is_k = !is_q && c < 2 * qd;
   const int width = (c < 2 * qd) ? qd : vd;
   const int col = is_q ? c : (is_k ? c - qd : c - 2 * qd);
   bf16* hi_plane = is_q ? q_hi : (is_k ? k_hi : v_hi);
   bf16* lo_plane = is_k ? k_lo : v_lo;
+  // the ring after T tokens (raw rows T-3, T-2, T-1), read before the loop
+  // writes nothing the block needs: only the first token block writes it
+  float nr[kRows][CPT];
+  if (tb0 == 0) {
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) hist(T - kRows + j, nr[j]);
+  }
   for (int tb = tb0; tb < tend; tb += kConvBatch) {
     // a batch of rows in flight at once (clamped, so the loads stay unconditional)
-    Row xs[kConvBatch];
+    float xs[kConvBatch][CPT];
 #pragma unroll
-    for (int i = 0; i < kConvBatch; ++i) xs[i] = load_x(min(tb + i, T - 1));
+    for (int i = 0; i < kConvBatch; ++i) load_x(min(tb + i, T - 1), xs[i]);
 #pragma unroll
     for (int u = 0; u < kConvBatch; ++u) {
       const int t = tb + u;
       if (t >= tend) break;
-      const Row& x = xs[u];
       float y[CPT];
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        float acc = h0.v[i] * w[i][0];
-        acc += h1.v[i] * w[i][1];
-        acc += h2.v[i] * w[i][2];
-        acc += x.v[i] * w[i][3];
+        float acc = h0[i] * w[i][0];
+        acc += h1[i] * w[i][1];
+        acc += h2[i] * w[i][2];
+        acc += xs[u][i] * w[i][3];
         y[i] = silu_f(acc);
       }
-      Raw hw, lw;
-      uint32_t* hp = reinterpret_cast<uint32_t*>(&hw);
-      uint32_t* lp = reinterpret_cast<uint32_t*>(&lw);
+      uint32_t hp[NW], lp[NW];
 #pragma unroll
       for (int e = 0; e < NW; ++e) hp[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
       const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
+      Raw hw;
+      if constexpr (CPT == 8) hw = u32x4{hp[0], hp[1], hp[2], hp[3]};
+      else hw = uint2{hp[0], hp[1]};
       *reinterpret_cast<Raw*>(hi_plane + o) = hw;
       if (!is_q) {
         float r[CPT];
@@ -487,24 +496,27 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
           r[i] = y[i] - __uint_as_float((i & 1) ? (hp[i >> 1] & 0xffff0000u) : (hp[i >> 1] << 16));
 #pragma unroll
         for (int e = 0; e < NW; ++e) lp[e] = pack_bf16x2(r[2 * e], r[2 * e + 1]);
+        Raw lw;
+        if constexpr (CPT == 8) lw = u32x4{lp[0], lp[1], lp[2], lp[3]};
+        else lw = uint2{lp[0], lp[1]};
         *reinterpret_cast<Raw*>(lo_plane + o) = lw;
       }
-      h0 = h1;
-      h1 = h2;
-      h2 = x;
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        h0[i] = h1[i];
+        h1[i] = h2[i];
+        h2[i] = xs[u][i];
+      }
     }
   }
   if (tb0 == 0) {
     // the ring after T tokens: raw rows T-3, T-2, T-1 at rows (head + T + j) % 3
-    Row nr[kRows];
-#pragma unroll
-    for (int j = 0; j < kRows; ++j) nr[j] = hist(T - kRows + j);
 #pragma unroll
     for (int j = 0; j < kRows; ++j)
 #pragma unroll
       for (int v4 = 0; v4 < CPT / 4; ++v4)
         *reinterpret_cast<f32x4*>(ring + static_cast<size_t>((head + T + j) % kRows) * ch + v4 * 4) =
-            f32x4{nr[j].v[v4 * 4], nr[j].v[v4 * 4 + 1], nr[j].v[v4 * 4 + 2], nr[j].v[v4 * 4 + 3]};
+            f32x4{nr[j][v4 * 4], nr[j][v4 * 4 + 1], nr[j][v4 * 4 + 2], nr[j][v4 * 4 + 3]};
   }
 }
 
