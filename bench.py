@@ -542,6 +542,60 @@ def sub_deltanet_layer_prefill(torch, aila_amd, reps=10):
             "tok_per_s": round(T / (us * 1e-6))}
 
 
+def sub_paged_decode(torch, aila_amd, page_size=256, reps=32):
+    """One config-5 GQA layer (B=8, Hq=16, Hkv=4, D=256, L=32768) over a
+    paged cache (pages of page_size rows scattered in a shuffled pool) next
+    to the same rows in the contiguous layout; HIP events around `reps`
+    back-to-back launches each."""
+    B, Hq, Hkv, D, L = B5, GQA_HQ, GQA_HKV, GQA_D, L5
+    mp = L // page_size
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 8)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    pk = torch.empty((B * mp, Hkv, page_size, D), **bf).normal_(generator=g)
+    pv = torch.empty_like(pk).normal_(generator=g)
+    table = torch.randperm(B * mp, generator=torch.Generator().manual_seed(7)).to(torch.int32).view(B, mp).cuda()
+    q = torch.randn((B, Hq, D), generator=g, **bf)
+    lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    fn = lambda: aila_amd.gqa_decode_paged(q, pk, pv, table, lens, L, out=out, workspace=ws)
+    res = {}
+    for name, f in (("paged", fn),):
+        for _ in range(3):
+            f()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(2.4e9 * 0.01))
+        s.record()
+        for _ in range(reps):
+            f()
+        e.record()
+        torch.cuda.synchronize()
+        res[name + "_us"] = round(s.elapsed_time(e) / reps * 1e3, 2)
+    del pk, pv
+    kc = torch.empty((B, Hkv, L, D), **bf).normal_(generator=g)
+    vc = torch.empty_like(kc).normal_(generator=g)
+    f = lambda: aila_amd.gqa_decode(q, kc, vc, L, out=out, workspace=ws, seq_lens=lens)
+    for _ in range(3):
+        f()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.4e9 * 0.01))
+    s.record()
+    for _ in range(reps):
+        f()
+    e.record()
+    torch.cuda.synchronize()
+    res["contiguous_us"] = round(s.elapsed_time(e) / reps * 1e3, 2)
+    byts = gqa_bytes(B, Hq, Hkv, D, L)
+    res["paged_GBps"] = round(byts / res["paged_us"] / 1e3, 1)
+    res["contiguous_GBps"] = round(byts / res["contiguous_us"] / 1e3, 1)
+    res["config"] = f"config-5 GQA layer B={B} L={L} over {page_size}-row pages (shuffled pool) vs contiguous"
+    del kc, vc
+    return res
+
+
 def sub_decode_cfg1(torch, aila_amd, per_graph=32, reps=20):
     B, Hq, Hkv, D, L = 1, 16, 8, 128, 512
     g = torch.Generator(device="cuda")
@@ -690,7 +744,7 @@ def main():
     ap.add_argument("--no-sub", action="store_true", help="skip the config 1-4 sub-metrics")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
-                    choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill",
+                    choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill", "paged_decode",
                              "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
@@ -712,6 +766,7 @@ def main():
          "deltanet_layer_decode": lambda t, a: sub_deltanet_layer_decode(t, a, steps=320),
          "deltanet_layer_prefill": lambda t, a: sub_deltanet_layer_prefill(t, a, reps=10),
          "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20),
+         "paged_decode": lambda t, a: sub_paged_decode(t, a),
          "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a)}[args.profile_kernel](torch, aila_amd)
         if r:
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
@@ -737,6 +792,8 @@ def main():
         log(f"[bench] deltanet layer prefill {sub['deltanet_layer_prefill']}")
         log(f"[bench] deltanet prefill {sub['deltanet_prefill']}")
         sub["gqa_decode_cfg1"] = sub_decode_cfg1(torch, aila_amd)
+        sub["paged_decode"] = sub_paged_decode(torch, aila_amd)
+        log(f"[bench] paged decode {sub['paged_decode']}")
         sub["decode_prep"] = sub_decode_prep(torch, aila_amd)
         log(f"[bench] decode prep {sub['decode_prep']}")
         sub["fused_prep_decode"] = sub_fused_prep_decode(torch, aila_amd)
