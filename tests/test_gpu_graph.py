@@ -60,3 +60,62 @@ def test_graph_replay_matches_eager():
         assert torch.equal(graph_s["lens"], eager["lens"])
     assert torch.equal(graph_s["kc"], eager["kc"]) and torch.equal(graph_s["vc"], eager["vc"])
     assert int(eager["lens"][0]) == L0 + 7
+
+
+def test_graph_replay_paged_decode_and_wide_layer_decode():
+    """A decode step over the paged cache (paged append + paged decode with
+    device lengths) and the whole DeltaNet layer with one workgroup per value
+    head (self-resetting arrival counts), captured once and replayed: every
+    replay equals the eager step, and the arrival counts are zero after
+    each."""
+    import torch
+    import aila_amd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(321)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    B, Hq, Hkv, D, page, mp, L0 = 2, 8, 2, 128, 64, 8, 300
+    Hk, Hv, d = 2, 4, 128
+    ch = 2 * Hk * d + Hv * d
+    pk0 = torch.randn((B * mp, Hkv, page, D), generator=g, **bf)
+    pv0 = torch.randn((B * mp, Hkv, page, D), generator=g, **bf)
+    table = torch.randperm(B * mp, generator=torch.Generator().manual_seed(5)).to(torch.int32).view(B, mp).cuda()
+    st0 = torch.randn((B, Hv, d, d), generator=g, device="cuda") * 0.02
+    cs0 = torch.randn((B, 3, ch), generator=g, device="cuda")
+    w = torch.randn((ch, 4), generator=g, **bf)
+    nw = torch.ones(d, device="cuda")
+    x = dict(q=torch.randn((B, Hq, D), generator=g, **bf), kn=torch.randn((B, Hkv, D), generator=g, **bf),
+             vn=torch.randn((B, Hkv, D), generator=g, **bf), qkv=torch.randn((B, ch), generator=g, **bf),
+             z=torch.randn((B, Hv * d), generator=g, **bf), a=torch.randn((B, Hv), generator=g, **bf),
+             b=torch.randn((B, Hv), generator=g, **bf))
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+
+    def make_state():
+        return dict(pk=pk0.clone(), pv=pv0.clone(), st=st0.clone(), cs=cs0.clone(),
+                    pos=torch.full((B,), L0, dtype=torch.int32, device="cuda"),
+                    lens=torch.full((B,), L0 + 1, dtype=torch.int32, device="cuda"),
+                    heads=torch.zeros((B,), dtype=torch.int32, device="cuda"),
+                    arr=torch.zeros((B * Hk,), dtype=torch.int32, device="cuda"),
+                    o=torch.empty((B, Hq, D), **bf), lo=torch.empty((B, Hv * d), **bf))
+
+    def step(S):
+        aila_amd.kv_append_paged(x["kn"], x["vn"], S["pk"], S["pv"], table, S["pos"])
+        aila_amd.gqa_decode_paged(x["q"], S["pk"], S["pv"], table, S["lens"], page * mp, out=S["o"], workspace=ws)
+        aila_amd.deltanet_layer_decode(x["qkv"], x["z"], x["a"], x["b"], w, S["cs"], 0, nw, S["st"], Hk,
+                                       out=S["lo"], conv_heads=S["heads"], arrivals=S["arr"])
+        S["pos"].add_(1)
+        S["lens"].add_(1)
+        S["heads"].add_(1).remainder_(3)
+
+    eager, graph_s = make_state(), make_state()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        step(graph_s)
+    torch.cuda.synchronize()
+    for i in range(5):
+        step(eager)
+        gr.replay()
+        torch.cuda.synchronize()
+        _ = (eager["o"].float().sum() + 1).item()
+        for key in ("o", "lo", "st", "cs", "pk", "pv", "lens", "heads"):
+            assert torch.equal(graph_s[key], eager[key]), f"replay {i}: {key} differs"
+        assert not graph_s["arr"].any() and not eager["arr"].any()
