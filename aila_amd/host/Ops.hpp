@@ -31,6 +31,16 @@ void attention_decode(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache,
                       Tensor& scores_buf, int num_heads, int num_kv_heads, int head_dim,
                       int cached_len, Tensor* exact_partials_buf = nullptr);
 
+// The same decode over a paged KV cache (an addition behind the same shim;
+// the reference keeps one contiguous cache per sequence): k_pages/v_pages
+// [num_pages, Hkv, page_size, D] bf16, block_table s32 [B, max_pages] (row
+// t of sequence b is row t % page_size of page block_table[b][t /
+// page_size]), seq_lens s32 [B]; q/output [B, Hq*D]. max_len bounds every
+// seq_lens[b]; page_size is a multiple of 16. exact_partials_buf as above.
+void attention_decode_paged(Context& ctx, Tensor& q, Tensor& k_pages, Tensor& v_pages, Tensor& block_table,
+                            Tensor& seq_lens, Tensor& output, int num_heads, int num_kv_heads, int head_dim,
+                            int max_len, Tensor* exact_partials_buf = nullptr);
+
 // Causal prefill over the current chunk (Ops.hpp:271-282). q [S, Hq*D],
 // k/v [S, Hkv*D]; output [S, Hq*D]. scores_buf is accepted and unused (no
 // [H, S, S] score matrix is materialised).

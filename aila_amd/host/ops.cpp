@@ -58,6 +58,32 @@ void attention_decode(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache,
         "attention_decode");
 }
 
+void attention_decode_paged(Context& ctx, Tensor& q, Tensor& k_pages, Tensor& v_pages, Tensor& block_table,
+                            Tensor& seq_lens, Tensor& output, int num_heads, int num_kv_heads, int head_dim,
+                            int max_len, Tensor* exact_partials_buf) {
+  need_dtype(q, DType::bf16, "attention_decode_paged q");
+  need_dtype(k_pages, DType::bf16, "attention_decode_paged k_pages");
+  need_dtype(v_pages, DType::bf16, "attention_decode_paged v_pages");
+  need_dtype(output, DType::bf16, "attention_decode_paged output");
+  need_dtype(block_table, DType::s32, "attention_decode_paged block_table");
+  need_dtype(seq_lens, DType::s32, "attention_decode_paged seq_lens");
+  const int B = static_cast<int>(block_table.shape(0));
+  const int max_pages = static_cast<int>(block_table.shape(1));
+  const int page_size = static_cast<int>(k_pages.shape(2));
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (exact_partials_buf && exact_partials_buf->valid() &&
+      exact_partials_buf->size_bytes() >= 2 * static_cast<size_t>(B) * num_heads * (16 + head_dim) * sizeof(float)) {
+    ws = exact_partials_buf->data();
+    ws_bytes = exact_partials_buf->size_bytes();
+  }
+  check(aila_hip_gqa_decode_paged(q.data(), k_pages.data(), v_pages.data(), output.data(), ws, ws_bytes, B,
+                                  num_heads, num_kv_heads, head_dim, page_size,
+                                  static_cast<const int*>(block_table.data()), max_pages, max_len,
+                                  static_cast<const int*>(seq_lens.data()), ctx.stream()),
+        "attention_decode_paged");
+}
+
 void attention_prefill(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& output,
                        Tensor& scores_buf, int seq_len, int num_heads, int num_kv_heads,
                        int head_dim) {

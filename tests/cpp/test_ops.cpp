@@ -359,6 +359,46 @@ int main() {
     expect(es <= 1e-3 && eo <= 1e-2 && download<float>(ctx, tcs) == csw && head == (1 + T) % 3,
            "linear_delta_layer prefill + decode", std::fmax(es, eo));
   }
+  // ---- attention_decode_paged: a shuffled page pool against the oracle -----
+  {
+    const int B = 2, Hq = 16, Hkv = 4, D = 256, page = 64, mp = 16, max_seq = page * mp;
+    const int lens[B] = {700, 1024};
+    const int npages = B * mp;
+    u16v q = rand_bf16(size_t(B) * Hq * D);
+    std::vector<u16v> kc(B), vc(B);
+    u16v pk(size_t(npages) * Hkv * page * D), pv(pk.size());
+    std::vector<int> table(size_t(B) * mp);
+    for (int b = 0; b < B; ++b) {
+      kc[b] = rand_bf16(size_t(Hkv) * max_seq * D);
+      vc[b] = rand_bf16(size_t(Hkv) * max_seq * D);
+      for (int j = 0; j < mp; ++j) {
+        const int pg = ((b * mp + j) * 5) % npages;   // a permutation of the pool (gcd(5, 32) = 1)
+        table[size_t(b) * mp + j] = pg;
+        for (int h = 0; h < Hkv; ++h)
+          std::memcpy(&pk[((size_t(pg) * Hkv + h) * page) * D], &kc[b][(size_t(h) * max_seq + j * page) * D],
+                      size_t(page) * D * 2),
+          std::memcpy(&pv[((size_t(pg) * Hkv + h) * page) * D], &vc[b][(size_t(h) * max_seq + j * page) * D],
+                      size_t(page) * D * 2);
+      }
+    }
+    Tensor tq = upload(ctx, q, {B, Hq * D}, DType::bf16);
+    Tensor tpk = upload(ctx, pk, {npages, Hkv, page, D}, DType::bf16), tpv = upload(ctx, pv, {npages, Hkv, page, D}, DType::bf16);
+    Tensor ttab = upload(ctx, table, {B, mp}, DType::s32);
+    std::vector<int> lv(lens, lens + B);
+    Tensor tlens = upload(ctx, lv, {B}, DType::s32);
+    Tensor out = Tensor::allocate(ctx, {B, Hq * D});
+    Tensor partials = Tensor::allocate(ctx, {B, Hq, mp, 16 + D}, DType::f32);
+    ops::attention_decode_paged(ctx, tq, tpk, tpv, ttab, tlens, out, Hq, Hkv, D, max_seq, &partials);
+    u16v got = download<uint16_t>(ctx, out);
+    double e = 0;
+    for (int b = 0; b < B; ++b) {
+      u16v want(size_t(Hq) * D), gb(got.begin() + size_t(b) * Hq * D, got.begin() + size_t(b + 1) * Hq * D);
+      orc_attention_decode_baseline(&q[size_t(b) * Hq * D], kc[b].data(), vc[b].data(), want.data(), 1, Hq, Hkv, D,
+                                    max_seq, lens[b]);
+      e = std::fmax(e, relerr(gb, want));
+    }
+    expect(e <= 1e-2, "attention_decode_paged (shuffled pool)", e);
+  }
   // ---- the backend-shaped caller: prefill 40 tokens, then decode one ------
   {
     using namespace backend_shape;
