@@ -85,7 +85,7 @@ def test_prefill_config2_qwen3_4b():
 
 @pytest.mark.parametrize("S", [1, 2, 17, 64, 127, 128, 129, 300])
 def test_prefill_ragged_lengths(S):
-    _prefill_case(5000 + S, S, 8, 2, 128)
+    _prefill_case(5000 + S, S, 8, 2, 128, with_cache=True, cache_pos=S % 7)
 
 
 @pytest.mark.parametrize("D,Hq,Hkv", [(64, 4, 4), (64, 8, 1), (256, 8, 2), (256, 16, 4), (128, 16, 16)])
@@ -95,7 +95,7 @@ def test_prefill_shapes(D, Hq, Hkv):
 
 def test_prefill_qwen35_full_attention_shape():
     # Qwen3.5 full-attention layer: 16 q / 4 kv heads, D=256, S=1024
-    _prefill_case(6100, 1024, 16, 4, 256, prepped=True)
+    _prefill_case(6100, 1024, 16, 4, 256, with_cache=True, cache_pos=11, prepped=True)
 
 
 @pytest.mark.parametrize("S,start,D", [(1, 100, 128), (37, 91, 128), (256, 1000, 128), (64, 64, 256),
