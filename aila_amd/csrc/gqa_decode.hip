@@ -74,6 +74,18 @@ struct PageArgs {
   int max_pages;
 };
 
+// Rows per split of one sequence. With a host length the host plan's
+// split_len holds. With device lengths the launch is sized for a bound (the
+// capacity a captured graph replays with), so the launched nsplit splits
+// share the sequence's actual rows evenly instead, in whole 16-row chunks:
+// no split then streams more than ~1/nsplit of the rows. The merge derives
+// the same value.
+__device__ __forceinline__ int split_rows(int len, int split_len, int nsplit, bool device_len) {
+  if (!device_len) return split_len;
+  const int per = (len + nsplit - 1) / nsplit;
+  return max(kChunk, (per + kChunk - 1) / kChunk * kChunk);
+}
+
 template <int D, int G, bool PREP = false, bool PAGED = false>
 __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kc,
@@ -95,11 +107,12 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   int len = L;
   if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
-  const int s0 = split * split_len;
-  const int nsplit_b = (len + split_len - 1) / split_len;
+  const int sl = split_rows(len, split_len, static_cast<int>(gridDim.x), seq_lens != nullptr);
+  const int s0 = split * sl;
+  const int nsplit_b = (len + sl - 1) / sl;
   const bool single = (part == nullptr);
   if (!single && split >= nsplit_b) return;   // the merge reads nsplit_b records
-  const int s1 = min(s0 + split_len, len);
+  const int s1 = min(s0 + sl, len);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m16 = lane & 15, g4 = lane >> 4;
@@ -472,13 +485,14 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 template <int D>
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
     const float* __restrict__ part, bf16* __restrict__ out, int Hq, int L,
-    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max) {
+    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit, int nsplit_max) {
   constexpr int C4 = D / 4;             // float4 columns
   constexpr int P = 256 / C4;           // split phases
   const int hq = blockIdx.x, b = blockIdx.y;
   int len = L;
   if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
-  const int ns = (len + split_len - 1) / split_len;
+  const int sl = split_rows(len, split_len, nsplit, seq_lens != nullptr);
+  const int ns = (len + sl - 1) / sl;
   const float* rec0 = part + (static_cast<size_t>(b) * Hq + hq) * nsplit_max * (kRecHeader + D);
   __shared__ float s_f[kMaxSplits];
   __shared__ float s_inv;
@@ -587,7 +601,7 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
                        a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
   if (a.part) {
     hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
-                       a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit_max);
+                       a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit, a.nsplit_max);
   }
   return check_launch("gqa_decode");
 }
