@@ -118,11 +118,11 @@ def build_config5(torch, aila_amd, steps, warmup):
     ws = torch.empty(aila_amd.gqa_decode_workspace_size(B5, GQA_HQ, GQA_D), dtype=torch.uint8, device=dev)
     gqa_out = torch.empty((B5, GQA_HQ, GQA_D), **bf)
     dn_out = torch.empty((B5, DN_HV, DN_D), **bf)
-    # device-side lengths: positions = row written this step, lens = rows attended
+    # device-side lengths: positions = row written this step (rows attended:
+    # positions + 1)
     positions = torch.full((B5,), L5, dtype=torch.int32, device=dev)
-    lens = torch.full((B5,), L5 + 1, dtype=torch.int32, device=dev)
     return dict(kc=kc, vc=vc, states=states, pool=pool, ws=ws, gqa_out=gqa_out, dn_out=dn_out,
-                positions=positions, lens=lens, max_seq=max_seq)
+                positions=positions, max_seq=max_seq)
 
 
 def step5(aila_amd, W, p):
@@ -139,7 +139,6 @@ def step5(aila_amd, W, p):
                                      out=W["dn_out"])
             di += 1
     W["positions"].add_(1)
-    W["lens"].add_(1)
 
 
 def bench_config5(torch, aila_amd, steps, warmup):
@@ -154,7 +153,6 @@ def bench_config5(torch, aila_amd, steps, warmup):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     W["positions"].fill_(L5)
-    W["lens"].fill_(L5 + 1)
     for p in range(NPOOL):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -164,7 +162,7 @@ def bench_config5(torch, aila_amd, steps, warmup):
     for i in range(warmup):
         graphs[i % NPOOL].replay()
     torch.cuda.synchronize()
-    L_first = int(W["lens"][0].item())
+    L_first = int(W["positions"][0].item()) + 1
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -745,7 +743,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
                     choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill", "paged_decode",
-                             "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode"],
+                             "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode",
+                             "stack"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     args = ap.parse_args()
@@ -767,7 +766,8 @@ def main():
          "deltanet_layer_prefill": lambda t, a: sub_deltanet_layer_prefill(t, a, reps=10),
          "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20),
          "paged_decode": lambda t, a: sub_paged_decode(t, a),
-         "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a)}[args.profile_kernel](torch, aila_amd)
+         "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a),
+         "stack": lambda t, a: {k: v for k, v in bench_config5(t, a, 32, 4).items() if k != "W"}}[args.profile_kernel](torch, aila_amd)
         if r:
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
         return
