@@ -72,7 +72,10 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
  * engines that allocate the cache in fixed-size pages.
  *   k_pages, v_pages  [num_pages, Hkv, page_size, D] bf16 page pool
  *   block_table       device int[B, max_pages]: row t of sequence b is row
- *                     t % page_size of page block_table[b*max_pages + t/page_size]
+ *                     t % page_size of page block_table[b*max_pages + t/page_size].
+ *                     Entries covering rows < seq_lens[b] must index the pool
+ *                     (the kernel dereferences only those); the rest, e.g. -1
+ *                     for unallocated pages, are never used as addresses.
  *   seq_lens          device int[B] (required): sequence b attends rows
  *                     [0, min(seq_lens[b], max_len))
  *   max_len           host bound on every seq_lens[b] (<= max_pages*page_size);
@@ -90,7 +93,8 @@ int aila_hip_gqa_decode_paged(const void* q, const void* k_pages,
 /* Append one token's K/V row per sequence into its page: k_new/v_new
  * [B, Hkv, D] bf16 go to row positions[b] (device int[B]) of sequence b in
  * the paged layout of aila_hip_gqa_decode_paged. Positions outside
- * [0, max_pages*page_size) are skipped. (The paged counterpart of the cache
+ * [0, max_pages*page_size) are skipped; the table entry of every other
+ * position must index the pool. (The paged counterpart of the cache
  * write of ops::decode_prepare_qkv, src/ops/ElementwiseOps.cpp:105-216.) */
 int aila_hip_kv_append_paged(const void* k_new, const void* v_new,
                              void* k_pages, void* v_pages, int B, int Hkv,
