@@ -37,6 +37,8 @@ _SIGS = {
     "aila_hip_kv_append": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_prefill": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_gqa_prefill_cached": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "aila_hip_gqa_prefill_cached_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
+    "aila_hip_gqa_prefill_cached_ws": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_copy_to_cache": ([_P, _P, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_deltanet_decode": ([_P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _F, _F, _P], _I),
@@ -284,8 +286,15 @@ def gqa_prefill(q, k, v, Hq: int, Hkv: int, out=None, k_cache=None, v_cache=None
     return out
 
 
-def gqa_prefill_cached(q, k_cache, v_cache, start_pos: int, Hq: int, out=None, stream=None):
-    """q [S, Hq*D] at positions start_pos.. attends cache [Hkv, max_seq, D]."""
+def gqa_prefill_cached_workspace_size(S: int, start_pos: int, Hq: int, Hkv: int, D: int) -> int:
+    """Bytes of the key-split workspace gqa_prefill_cached would use (0: none)."""
+    return int(lib().aila_hip_gqa_prefill_cached_workspace_size(S, start_pos, Hq, Hkv, D))
+
+
+def gqa_prefill_cached(q, k_cache, v_cache, start_pos: int, Hq: int, out=None, workspace=None, stream=None):
+    """q [S, Hq*D] at positions start_pos.. attends cache [Hkv, max_seq, D].
+    workspace: a uint8 device tensor for the key split (see
+    gqa_prefill_cached_workspace_size), or None for no split."""
     import torch
     S = q.shape[0]
     Hkv, max_seq, D = k_cache.shape
@@ -295,8 +304,15 @@ def gqa_prefill_cached(q, k_cache, v_cache, start_pos: int, Hq: int, out=None, s
     if out is None:
         out = torch.empty_like(q)
     _need(out, torch.bfloat16, (S, Hq * D), "out")
-    rc = lib().aila_hip_gqa_prefill_cached(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), S,
-                                           int(start_pos), Hq, Hkv, D, max_seq, _stream(stream))
+    if workspace is None:
+        rc = lib().aila_hip_gqa_prefill_cached(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), S,
+                                               int(start_pos), Hq, Hkv, D, max_seq, _stream(stream))
+    else:
+        if not workspace.is_cuda or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous device tensor")
+        rc = lib().aila_hip_gqa_prefill_cached_ws(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                                  _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                                  S, int(start_pos), Hq, Hkv, D, max_seq, _stream(stream))
     _check(rc, "aila_hip_gqa_prefill_cached")
     return out
 

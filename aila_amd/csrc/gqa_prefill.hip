@@ -25,6 +25,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
 
 namespace aila {
 namespace {
@@ -102,13 +103,13 @@ __device__ __forceinline__ int swz_v(int r) {
 // 16-lane group, lane i addresses 4 bf16 of row kbase + i/4 at column
 // d0 + 4*(i%4), and lane j receives V[kbase+r][d0+j] for r = 0..3 - four
 // keys of one head dim, the A-operand layout.
-template <int D, int RPW, int BN>
+template <int D, int RPW, int BN, bool KSPLIT = false>
 __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     const bf16* __restrict__ q, int q_row_stride, const bf16* __restrict__ k,
     const bf16* __restrict__ v, int kv_row_stride, long kv_head_stride,
     bf16* __restrict__ out, int o_row_stride, int S, int start_pos, int Hkv,
     int G, float scale_log2, bf16* __restrict__ k_cache,
-    bf16* __restrict__ v_cache, int cache_pos, int max_seq) {
+    bf16* __restrict__ v_cache, int cache_pos, int max_seq, float* __restrict__ part) {
   using C = PrefillCfg<D, RPW, BN>;
   // K/V tiles per double-buffer slot, indexed by group.
   __shared__ __attribute__((aligned(1024))) unsigned char sK0[2][C::TILE];
@@ -129,21 +130,34 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs,
   // so consecutive logical ids (pairs of one head, then the heads of one KV
   // group) are gathered onto one XCD and its L2 holds that group's K/V.
-  const int nwg = npair * static_cast<int>(gridDim.y);
-  const int lin = blockIdx.x + npair * blockIdx.y;
+  // With a key split (gridDim.z > 1, partial records in `part`), slice z of
+  // the grid walks the z-th of gridDim.z equal runs of every query block's
+  // key blocks; the slices of the same KV group and key run stay together.
+  const int Hq = static_cast<int>(gridDim.y), nz = KSPLIT ? static_cast<int>(gridDim.z) : 1;
+  const int nwg = npair * Hq * nz;
+  const int lin = blockIdx.x + npair * (blockIdx.y + Hq * blockIdx.z);
   int logical = lin;
   if (nwg % kNumXcd == 0) logical = (lin % kNumXcd) * (nwg / kNumXcd) + lin / kNumXcd;
   const int pr = logical % npair;
-  const int h = logical / npair;
+  const int h = (logical / npair) % Hq;
+  const int zs = KSPLIT ? logical / (npair * Hq) : 0;
   const int kvh = h / G;
   const int ql = pr, qh = nqb - 1 - pr;                  // light / heavy query block
   auto nkeyblk = [&](int qb) __attribute__((always_inline)) { return (start_pos + min((qb + 1) * C::BM, S) - 1) / BN + 1; };
-  const int nl = (ql < qh) ? nkeyblk(ql) : 0;           // a middle block pairs with itself
-  const int nh = nkeyblk(qh);
+  auto run_lo = [&](int qb) __attribute__((always_inline)) { return KSPLIT ? nkeyblk(qb) * zs / nz : 0; };
+  auto run_hi = [&](int qb) __attribute__((always_inline)) {
+    return KSPLIT ? nkeyblk(qb) * (zs + 1) / nz : nkeyblk(qb);
+  };
+  const int l0 = (ql < qh) ? run_lo(ql) : 0;
+  const int nl = (ql < qh) ? run_hi(ql) - l0 : 0;       // a middle block pairs with itself
+  const int h0 = run_lo(qh);
+  const int nh = run_hi(qh) - h0;
   const int tA = (nl + nh + 1) / 2, tB = nl + nh - tA;   // tA >= tB
   const int hsplit = tA - nl;                           // heavy key blocks walked by A
   const int my_n = grp == 0 ? tA : tB;
-  auto kb_of = [&](int it) __attribute__((always_inline)) { return grp == 0 ? (it < nl ? it : it - nl) : hsplit + it; };
+  auto kb_of = [&](int it) __attribute__((always_inline)) {
+    return grp == 0 ? (it < nl ? l0 + it : h0 + it - nl) : h0 + hsplit + it;
+  };
   auto qb_of = [&](int it) __attribute__((always_inline)) { return (grp == 0 && it < nl) ? ql : qh; };
   const int kv_len = start_pos + S;
   const bf16* Kh = k + kvh * kv_head_stride;
@@ -218,6 +232,22 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     }
   };
   auto store_segment = [&]() __attribute__((always_inline)) {
+    if (KSPLIT) {
+      // key split: the unnormalised state {m (log2 units), l, acc} of each
+      // row, stride D + 4 floats, slice-major
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) {
+        const int row = seg_qb * C::BM + wave * RPW + qt * 16 + m16;
+        if (row < S) {
+          float* rec = part + ((static_cast<size_t>(zs) * Hq + h) * S + row) * (D + 4);
+          if (g4 == 0) *reinterpret_cast<f32x4*>(rec) = f32x4{m_run[qt], l_run[qt], 0.f, 0.f};
+#pragma unroll
+          for (int dt = 0; dt < C::DT; ++dt)
+            *reinterpret_cast<f32x4*>(rec + 4 + dt * 16 + g4 * 4) = o_acc[dt][qt];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int qt = 0; qt < C::QT; ++qt) {
       const float inv = 1.0f / l_run[qt];   // full row sum, held by every lane
@@ -307,7 +337,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     }
 #pragma unroll
     for (int qt = 0; qt < C::QT; ++qt) {
-      const float nm = -m_run[qt];
+      // every key so far masked (possible only when a key run starts past
+      // some rows' positions): p = 0, not exp2(-inf + inf)
+      const float nm = (KSPLIT && m_run[qt] == -INFINITY) ? 0.f : -m_run[qt];
 #pragma unroll
       for (int s2 = 0; s2 < C::PS; ++s2) {
         float p[8];
@@ -496,6 +528,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
             fa[qt] = (ma == -INFINITY) ? 0.f : fast_exp2(ma - M);
             fb[qt] = (m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - M);
             l_run[qt] = fa[qt] * la + fb[qt] * l_run[qt];
+            m_run[qt] = M;   // l and acc are now relative to M (a key-split record carries it)
           }
 #pragma unroll
           for (int dd = 0; dd < C::DT / 2; ++dd) {
@@ -516,34 +549,146 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   copy_rows_to_cache();
 }
 
+// Key-split merge: out row = sum_z 2^(m_z - M) acc_z / sum_z 2^(m_z - M) l_z
+// over the slices' partial records (M = max m_z; a slice whose keys were
+// all masked for the row has m = -inf and weight 0). D/4 threads per
+// (row, head), one float4 column each.
+template <int D>
+__global__ __launch_bounds__(256) void gqa_prefill_merge_kernel(const float* __restrict__ part,
+                                                                bf16* __restrict__ out, int o_row_stride, int S,
+                                                                int Hq, int nz) {
+  constexpr int TPR = D / 4;
+  constexpr int RPB = 256 / TPR;
+  const long idx = static_cast<long>(blockIdx.x) * RPB + threadIdx.x / TPR;   // row * Hq + h
+  if (idx >= static_cast<long>(S) * Hq) return;
+  const int row = static_cast<int>(idx / Hq), h = static_cast<int>(idx % Hq), c = (threadIdx.x % TPR) * 4;
+  const size_t slice = static_cast<size_t>(Hq) * S * (D + 4);
+  const float* rec = part + (static_cast<size_t>(h) * S + row) * (D + 4);
+  float M = -INFINITY;
+  for (int z = 0; z < nz; ++z) M = fmaxf(M, rec[z * slice]);
+  float L = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < nz; ++z) {
+    const float m = rec[z * slice];
+    const float w = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
+    L += w * rec[z * slice + 1];
+    acc += w * *reinterpret_cast<const f32x4*>(rec + z * slice + 4 + c);
+  }
+  const float inv = 1.0f / L;
+  *reinterpret_cast<u32x2*>(out + static_cast<size_t>(row) * o_row_stride + h * D + c) =
+      u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+}
+
 template <int D, int RPW, int BN>
 int launch_prefill(const bf16* q, const bf16* k, const bf16* v, int kv_row_stride,
                    long kv_head_stride, bf16* out, int S, int start_pos, int Hq,
                    int Hkv, bf16* k_cache, bf16* v_cache, int cache_pos, int max_seq,
-                   hipStream_t st) {
+                   int nz, float* part, hipStream_t st) {
   using C = PrefillCfg<D, RPW, BN>;
   const int nqb = (S + C::BM - 1) / C::BM;
   const int npair = (nqb + 1) / 2;
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-  hipLaunchKernelGGL((gqa_prefill_kernel<D, RPW, BN>), dim3(npair, Hq), dim3(2 * kThreads), 0, st,
-                     q, Hq * D, k, v, kv_row_stride, kv_head_stride, out, Hq * D, S, start_pos,
-                     Hkv, Hq / Hkv, scale_log2, k_cache, v_cache, cache_pos, max_seq);
+  if (nz < 2) {
+    nz = 1;
+    part = nullptr;
+  }
+  if (part == nullptr)
+    hipLaunchKernelGGL((gqa_prefill_kernel<D, RPW, BN, false>), dim3(npair, Hq), dim3(2 * kThreads), 0, st,
+                       q, Hq * D, k, v, kv_row_stride, kv_head_stride, out, Hq * D, S, start_pos,
+                       Hkv, Hq / Hkv, scale_log2, k_cache, v_cache, cache_pos, max_seq, nullptr);
+  else
+    hipLaunchKernelGGL((gqa_prefill_kernel<D, RPW, BN, true>), dim3(npair, Hq, nz), dim3(2 * kThreads), 0, st,
+                       q, Hq * D, k, v, kv_row_stride, kv_head_stride, out, Hq * D, S, start_pos,
+                       Hkv, Hq / Hkv, scale_log2, nullptr, nullptr, 0, max_seq, part);
+  if (part != nullptr) {
+    constexpr int RPB = 256 / (D / 4);
+    const long rows = static_cast<long>(S) * Hq;
+    hipLaunchKernelGGL((gqa_prefill_merge_kernel<D>), dim3(static_cast<unsigned>((rows + RPB - 1) / RPB)),
+                       dim3(256), 0, st, part, out, Hq * D, S, Hq, nz);
+  }
   return check_launch("gqa_prefill");
+}
+
+template <int D>
+struct PrefillShape;
+template <>
+struct PrefillShape<64> { static constexpr int RPW = 32, BN = 64; };
+template <>
+struct PrefillShape<128> { static constexpr int RPW = 32, BN = 64; };
+template <>
+struct PrefillShape<256> { static constexpr int RPW = 16, BN = 32; };
+
+// Prefill workgroups the device holds at once, per device (idempotent,
+// computed on first use).
+template <int D>
+int prefill_resident() {
+  using PS = PrefillShape<D>;
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+  const int known = cache[dev].load(std::memory_order_relaxed);
+  if (known > 0) return known;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gqa_prefill_kernel<D, PS::RPW, PS::BN, true>, 2 * kThreads,
+                                                   0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 ||
+      cus <= 0)
+    return 256;
+  cache[dev].store(per_cu * cus, std::memory_order_relaxed);
+  return per_cu * cus;
+}
+
+constexpr int kMaxKeySplits = 16;
+
+// Key runs per query block for a prefill over a cached prefix: enough
+// workgroups for one round of the device, each run at least 4 key blocks
+// long (the short runs' per-workgroup start-up would cost more than they
+// save). 1 = no split.
+template <int D>
+int prefill_key_splits(int S, int start_pos, int Hq) {
+  using PS = PrefillShape<D>;
+  using C = PrefillCfg<D, PS::RPW, PS::BN>;
+  const int nqb = (S + C::BM - 1) / C::BM;
+  const int nwg = (nqb + 1) / 2 * Hq;
+  const int resident = prefill_resident<D>();
+  if (2 * nwg > resident) return 1;
+  const int min_blocks = (start_pos + std::min(C::BM, S) - 1) / PS::BN + 1;   // the first query block's keys
+  int nz = (resident + nwg - 1) / nwg;
+  nz = std::min(nz, std::min(kMaxKeySplits, min_blocks / 4));
+  return nz < 2 ? 1 : nz;
+}
+
+int key_splits_for(int D, int S, int start_pos, int Hq) {
+  switch (D) {
+    case 64: return prefill_key_splits<64>(S, start_pos, Hq);
+    case 128: return prefill_key_splits<128>(S, start_pos, Hq);
+    case 256: return prefill_key_splits<256>(S, start_pos, Hq);
+    default: return 1;
+  }
+}
+
+size_t key_split_bytes(int nz, int S, int Hq, int D) {
+  return static_cast<size_t>(nz) * Hq * S * (D + 4) * sizeof(float);
 }
 
 int dispatch_prefill(int D, const bf16* q, const bf16* k, const bf16* v, int kv_row_stride,
                      long kv_head_stride, bf16* out, int S, int start_pos, int Hq, int Hkv,
-                     bf16* k_cache, bf16* v_cache, int cache_pos, int max_seq, hipStream_t st) {
+                     bf16* k_cache, bf16* v_cache, int cache_pos, int max_seq, hipStream_t st,
+                     int nz = 1, float* part = nullptr) {
   switch (D) {
     case 64:
-      return launch_prefill<64, 32, 64>(q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos,
-                                        Hq, Hkv, k_cache, v_cache, cache_pos, max_seq, st);
+      return launch_prefill<64, PrefillShape<64>::RPW, PrefillShape<64>::BN>(
+          q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache, v_cache, cache_pos, max_seq,
+          nz, part, st);
     case 128:
-      return launch_prefill<128, 32, 64>(q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos,
-                                         Hq, Hkv, k_cache, v_cache, cache_pos, max_seq, st);
+      return launch_prefill<128, PrefillShape<128>::RPW, PrefillShape<128>::BN>(
+          q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache, v_cache, cache_pos, max_seq,
+          nz, part, st);
     case 256:
-      return launch_prefill<256, 16, 32>(q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos,
-                                         Hq, Hkv, k_cache, v_cache, cache_pos, max_seq, st);
+      return launch_prefill<256, PrefillShape<256>::RPW, PrefillShape<256>::BN>(
+          q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache, v_cache, cache_pos, max_seq,
+          nz, part, st);
     default:
       return set_error(AILA_HIP_EUNSUPPORTED, "gqa_prefill: D=%d not in {64,128,256}", D);
   }
@@ -583,19 +728,42 @@ extern "C" int aila_hip_gqa_prefill(const void* q, const void* k, const void* v,
                           max_seq, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int aila_hip_gqa_prefill_cached(const void* q, const void* k_cache, const void* v_cache,
-                                           void* out, int S, int start_pos, int Hq, int Hkv, int D,
-                                           int max_seq, void* stream) {
+extern "C" size_t aila_hip_gqa_prefill_cached_workspace_size(int S, int start_pos, int Hq, int Hkv, int D) {
+  using namespace aila;
+  if (S <= 0 || start_pos < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || (D != 64 && D != 128 && D != 256)) return 0;
+  const int nz = key_splits_for(D, S, start_pos, Hq);
+  return nz > 1 ? key_split_bytes(nz, S, Hq, D) : 0;
+}
+
+extern "C" int aila_hip_gqa_prefill_cached_ws(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                              void* workspace, size_t workspace_bytes, int S, int start_pos,
+                                              int Hq, int Hkv, int D, int max_seq, void* stream) {
   using namespace aila;
   AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_prefill_cached: null pointer");
   AILA_REQUIRE(S > 0 && start_pos >= 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq <= 65535,
                "gqa_prefill_cached: bad shape (S=%d start_pos=%d Hq=%d Hkv=%d)", S, start_pos, Hq, Hkv);
   AILA_REQUIRE(static_cast<long>(start_pos) + S <= max_seq,
                "gqa_prefill_cached: start_pos + S = %ld > max_seq=%d", static_cast<long>(start_pos) + S, max_seq);
+  AILA_REQUIRE(workspace == nullptr || reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "gqa_prefill_cached: workspace not 16-byte aligned");
+  int nz = 1;
+  if (workspace != nullptr && (D == 64 || D == 128 || D == 256)) {
+    nz = key_splits_for(D, S, start_pos, Hq);
+    // as many key runs as the workspace holds
+    const size_t per = key_split_bytes(1, S, Hq, D);
+    nz = static_cast<int>(std::min<size_t>(static_cast<size_t>(nz), workspace_bytes / per));
+  }
   return dispatch_prefill(D, static_cast<const bf16*>(q), static_cast<const bf16*>(k_cache),
                           static_cast<const bf16*>(v_cache), D, static_cast<long>(max_seq) * D,
                           static_cast<bf16*>(out), S, start_pos, Hq, Hkv, nullptr, nullptr, 0, max_seq,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<hipStream_t>(stream), nz, static_cast<float*>(workspace));
+}
+
+extern "C" int aila_hip_gqa_prefill_cached(const void* q, const void* k_cache, const void* v_cache,
+                                           void* out, int S, int start_pos, int Hq, int Hkv, int D,
+                                           int max_seq, void* stream) {
+  return aila_hip_gqa_prefill_cached_ws(q, k_cache, v_cache, out, nullptr, 0, S, start_pos, Hq, Hkv, D, max_seq,
+                                        stream);
 }
 
 extern "C" int aila_hip_copy_to_cache(const void* new_kv, void* cache, int S, int start_pos, int H,

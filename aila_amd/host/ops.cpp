@@ -107,11 +107,13 @@ void attention_prefill_write_cache(Context& ctx, Tensor& q, Tensor& k, Tensor& v
 void attention_prefill_cached(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache,
                               Tensor& output, Tensor& scores_buf, int seq_len, int start_pos,
                               int num_heads, int num_kv_heads, int head_dim, int max_seq_len) {
-  (void)scores_buf;
   need_dtype(q, DType::bf16, "attention_prefill_cached q");
-  check(aila_hip_gqa_prefill_cached(q.data(), k_cache.data(), v_cache.data(), output.data(), seq_len,
-                                    start_pos, num_heads, num_kv_heads, head_dim, max_seq_len,
-                                    ctx.stream()),
+  // The reference's score buffer ([heads, seq, total] fp32, never
+  // materialised here) serves as the key-split workspace.
+  const bool ws = scores_buf.valid();
+  check(aila_hip_gqa_prefill_cached_ws(q.data(), k_cache.data(), v_cache.data(), output.data(),
+                                       ws ? scores_buf.data() : nullptr, ws ? scores_buf.size_bytes() : 0, seq_len,
+                                       start_pos, num_heads, num_kv_heads, head_dim, max_seq_len, ctx.stream()),
         "attention_prefill_cached");
 }
 

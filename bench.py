@@ -278,6 +278,51 @@ def sub_prefill(torch, aila_amd, reps=20):
             "tflops": round(flops / us / 1e6, 1), "frac_of_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
 
 
+def sub_prefill_cached(torch, aila_amd, reps=20):
+    """Multi-turn prefill over a cached prefix (next row 3 of the path):
+    a Qwen3.5 full-attention layer (16 q / 4 kv heads, D=256) appends a
+    512-token turn to a 4096-token cache and attends it causally, then the
+    gated-attention epilogue out *= sigmoid(gate)."""
+    S, start, Hq, Hkv, D = 512, 4096, 16, 4, 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 6)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    max_seq = start + S
+    kc = torch.randn((Hkv, max_seq, D), generator=g, **bf)
+    vc = torch.randn((Hkv, max_seq, D), generator=g, **bf)
+    q = torch.randn((S, Hq * D), generator=g, **bf)
+    gate = torch.randn((S, Hq * D), generator=g, **bf)
+    out = torch.empty_like(q)
+
+    ws = torch.empty(max(aila_amd.gqa_prefill_cached_workspace_size(S, start, Hq, Hkv, D), 16), dtype=torch.uint8,
+                     device="cuda")
+
+    def timed(fn):
+        # HIP-graph replay of `reps` calls: the kernels' time, not the host's
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(reps):
+                fn()
+        gr.replay()
+        return time_graph(torch, gr, 3) * 1e3 / reps
+
+    us_split = timed(lambda: aila_amd.gqa_prefill_cached(q, kc, vc, start, Hq, out=out, workspace=ws))
+    us_whole = timed(lambda: aila_amd.gqa_prefill_cached(q, kc, vc, start, Hq, out=out))
+    us_gate = timed(lambda: aila_amd.sigmoid_mul(out, gate, out=out))
+    flops = 4 * D * Hq * (S * start + S * (S + 1) / 2)
+    gate_bytes = 3 * S * Hq * D * 2
+    return {"config": f"prefill over a cached prefix: S={S} new tokens after {start}, Hq={Hq} Hkv={Hkv} D={D}; "
+                      "then out *= sigmoid(gate)",
+            "attn_us": round(us_split, 2), "attn_tflops": round(flops / us_split / 1e6, 1),
+            "attn_frac_of_bf16_peak": round(flops / us_split / 1e6 / BF16_PEAK_TFLOPS, 4),
+            "key_split_workspace_bytes": int(ws.numel()) if ws.numel() > 16 else 0,
+            "attn_no_split_us": round(us_whole, 2),
+            "sigmoid_mul_us": round(us_gate, 2), "sigmoid_mul_GBps": round(gate_bytes / us_gate / 1e3, 1)}
+
+
 def sub_deltanet_decode(torch, aila_amd, steps=2048, per_graph=16):
     B, H, d = 32, 16, 128
     g = torch.Generator(device="cuda")
@@ -745,7 +790,7 @@ def main():
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
                     choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill", "paged_decode",
                              "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode",
-                             "stack"],
+                             "stack", "prefill_cached"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     args = ap.parse_args()
@@ -768,6 +813,7 @@ def main():
          "decode_prep": lambda t, a: sub_decode_prep(t, a, reps=20),
          "paged_decode": lambda t, a: sub_paged_decode(t, a),
          "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a),
+         "prefill_cached": lambda t, a: sub_prefill_cached(t, a),
          "stack": lambda t, a: {k: v for k, v in bench_config5(t, a, 32, 4).items() if k != "W"}}[args.profile_kernel](torch, aila_amd)
         if r:
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
@@ -784,6 +830,8 @@ def main():
     if not args.no_sub:
         sub["gqa_prefill"] = sub_prefill(torch, aila_amd)
         log(f"[bench] prefill {sub['gqa_prefill']}")
+        sub["prefill_cached"] = sub_prefill_cached(torch, aila_amd)
+        log(f"[bench] prefill cached {sub['prefill_cached']}")
         sub["deltanet_decode"] = sub_deltanet_decode(torch, aila_amd)
         log(f"[bench] deltanet decode {sub['deltanet_decode']}")
         sub["deltanet_layer_decode"] = sub_deltanet_layer_decode(torch, aila_amd)

@@ -193,6 +193,25 @@ int aila_hip_gqa_prefill_cached(const void* q, const void* k_cache,
                                 int start_pos, int Hq, int Hkv, int D,
                                 int max_seq, void* stream);
 
+/* The same prefill with a workspace, for a short turn over a long cached
+ * prefix: when the (query block pair, head) grid would leave the device
+ * mostly idle, each query block's keys are cut into runs walked by separate
+ * workgroups, whose partial softmax states {m, l, acc} (fp32, D + 4 floats
+ * per row and run) meet in a merge pass. The reference passes its score
+ * buffer scores_buf [heads, seq, total] fp32 here (ops::attention_prefill_cached,
+ * src/ops/Ops.hpp:293-298), which is far larger than the records need.
+ * workspace_size returns the bytes for the run count this call would use
+ * (0: no split); a smaller workspace gives fewer runs, a null one none.
+ * Results as aila_hip_gqa_prefill_cached within the attention tolerance
+ * (the runs' sums are added in another order). */
+size_t aila_hip_gqa_prefill_cached_workspace_size(int S, int start_pos,
+                                                  int Hq, int Hkv, int D);
+int aila_hip_gqa_prefill_cached_ws(const void* q, const void* k_cache,
+                                   const void* v_cache, void* out,
+                                   void* workspace, size_t workspace_bytes,
+                                   int S, int start_pos, int Hq, int Hkv,
+                                   int D, int max_seq, void* stream);
+
 /* ops::copy_to_cache (src/ops/Ops.hpp:199-201; AttentionOps.cpp:2513-2532):
  * new_kv [S, H*D] bf16 -> cache [H, max_seq, D] rows [start_pos, start_pos+S).
  * Requires D % 8 == 0 and 16-byte aligned pointers. */

@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "Ops.hpp"
+#include "aila_hip.h"
 
 extern "C" {
 void orc_attention_decode_baseline(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
@@ -210,6 +211,28 @@ int main() {
                                  max_seq, 0);
     e = relerr(download<uint16_t>(ctx, out2), want2);
     expect(e <= 1e-2, "attention_prefill_cached", e);
+  }
+  // ---- attention_prefill_cached with the reference's score buffer: a short
+  //      turn over a long prefix splits each query block's keys into runs ----
+  {
+    const int Hq = 16, Hkv = 4, D = 256, S = 100, start = 2100, max_seq = 2304;
+    const int total = start + S;
+    u16v kc = rand_bf16(size_t(Hkv) * max_seq * D), vc = rand_bf16(size_t(Hkv) * max_seq * D);
+    u16v q = rand_bf16(size_t(S) * Hq * D);
+    Tensor tk = upload(ctx, kc, {Hkv, max_seq, D}, DType::bf16), tv = upload(ctx, vc, {Hkv, max_seq, D}, DType::bf16);
+    Tensor tq = upload(ctx, q, {S, Hq * D}, DType::bf16), out = Tensor::allocate(ctx, {S, Hq * D});
+    Tensor scores = Tensor::allocate(ctx, {Hq, S, total}, DType::f32);   // as the backend sizes it
+    // one run's records: {m, l, pad, acc[D]} fp32 per (head, row); the score
+    // buffer holds total / (D + 4) runs, the split asks for up to 16
+    const size_t need = aila_hip_gqa_prefill_cached_workspace_size(S, start, Hq, Hkv, D);
+    const size_t per_run = size_t(Hq) * S * (D + 4) * sizeof(float);
+    expect(need >= 2 * per_run && scores.size_bytes() >= 2 * per_run,
+           "prefill_cached key split engages and scores_buf holds at least two runs", double(need / per_run));
+    ops::attention_prefill_cached(ctx, tq, tk, tv, out, scores, S, start, Hq, Hkv, D, max_seq);
+    u16v want(size_t(S) * Hq * D);
+    orc_attention_prefill_cached(q.data(), kc.data(), vc.data(), want.data(), S, start, Hq, Hkv, D, max_seq, 0);
+    const double e = relerr(download<uint16_t>(ctx, out), want);
+    expect(e <= 1e-2, "attention_prefill_cached (key runs through scores_buf)", e);
     // unsupported head_dim must throw
     bool threw = false;
     try {

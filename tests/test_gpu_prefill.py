@@ -118,6 +118,48 @@ def test_prefill_cached(S, start, D):
     assert _relerr(got, want) <= ATTN_TOL
 
 
+@pytest.mark.parametrize("S,start,Hq,Hkv,D", [(100, 2100, 16, 4, 256), (128, 3000, 16, 4, 256),
+                                               (200, 1500, 32, 8, 128), (37, 800, 8, 8, 128),
+                                               (64, 1000, 8, 1, 64)])
+def test_prefill_cached_key_split(S, start, Hq, Hkv, D):
+    """A short turn over a long prefix: with a workspace the keys of every
+    query block are cut into runs walked by separate workgroups and merged
+    (AttentionOps.cpp:2308-2507 semantics). Each run count the workspace
+    allows - the planned one, two, and none - matches the oracle; rows past
+    the attended range hold NaN."""
+    import torch
+    import aila_amd
+    max_seq = start + S + 9
+    seed = 7300 + S + D
+    print(f"prefill_cached key split S={S} start={start} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    kc = dg.normal_bf16(seed, 1, (Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 2, (Hkv, max_seq, D))
+    kc[:, start + S:] = 0x7FC0
+    vc[:, start + S:] = 0x7FC0
+    q = dg.normal_bf16(seed, 0, (S, Hq * D))
+    need = aila_amd.gqa_prefill_cached_workspace_size(S, start, Hq, Hkv, D)
+    assert need > 0, "a short turn over a long prefix should split its keys"
+    per_run = Hq * S * (D + 4) * 4
+    assert need % per_run == 0 and need // per_run >= 2
+    want = dg.bf16_to_f32(oracle.attention_prefill_cached(q, kc, vc, S, start, Hq, Hkv, D, max_seq))
+    dq, dk, dv = _t(q), _t(kc), _t(vc)
+    for nbytes in (need, 2 * per_run, per_run - 16):
+        ws = torch.full((nbytes // 4,), float("nan"), dtype=torch.float32, device="cuda").view(torch.uint8)
+        got = dg.bf16_to_f32(_np(aila_amd.gqa_prefill_cached(dq, dk, dv, start, Hq, workspace=ws)))
+        torch.cuda.synchronize()
+        assert np.isfinite(got).all(), nbytes
+        err = _relerr(got, want)
+        assert err <= ATTN_TOL, (nbytes, err)
+        rows = np.max(np.abs(got - want), axis=1) / np.maximum(np.max(np.abs(want), axis=1), 1e-30)
+        assert np.max(rows) <= 2 * ATTN_TOL, nbytes
+
+
+def test_prefill_cached_no_split_for_long_turns():
+    import aila_amd
+    # a 2048-token turn already fills the device: no workspace wanted
+    assert aila_amd.gqa_prefill_cached_workspace_size(2048, 4096, 32, 8, 128) == 0
+
+
 def test_copy_to_cache_bit_exact():
     import torch
     import aila_amd
