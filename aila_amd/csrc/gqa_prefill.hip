@@ -337,9 +337,10 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     }
 #pragma unroll
     for (int qt = 0; qt < C::QT; ++qt) {
-      // every key so far masked (possible only when a key run starts past
-      // some rows' positions): p = 0, not exp2(-inf + inf)
-      const float nm = (KSPLIT && m_run[qt] == -INFINITY) ? 0.f : -m_run[qt];
+      // every key so far masked (a walk that starts past some rows'
+      // positions: group B's first block, or a key run, over a cached prefix
+      // not aligned to the blocks): p = 0, not exp2(-inf + inf)
+      const float nm = (m_run[qt] == -INFINITY) ? 0.f : -m_run[qt];
 #pragma unroll
       for (int s2 = 0; s2 < C::PS; ++s2) {
         float p[8];

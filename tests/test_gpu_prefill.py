@@ -99,7 +99,8 @@ def test_prefill_qwen35_full_attention_shape():
 
 
 @pytest.mark.parametrize("S,start,D", [(1, 100, 128), (37, 91, 128), (256, 1000, 128), (64, 64, 256),
-                                       (130, 7, 64)])
+                                       (130, 7, 64),
+                                       (107, 109, 64)])   # group B's first key block lies past rows 0-18
 def test_prefill_cached(S, start, D):
     import torch
     import aila_amd
