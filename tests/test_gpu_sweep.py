@@ -1,10 +1,13 @@
 """Seeded sweeps of GPU parity over shapes and lengths the targeted tests do
-not pin one by one: split-K decode with device-side lengths (each sequence's
-rows shared evenly by the launched splits) and prefill over a cached prefix
-with and without the key split. Each case is checked against the CPU oracle
-(AttentionOps.cpp:73-166 for decode, :2308-2507 for the cached prefill)
-within the attention tolerance, with NaN in every cache row past the
-attended range."""
+not pin one by one, each case checked against the CPU oracle:
+  - split-K decode with device-side lengths (each sequence's rows shared
+    evenly by the launched splits), AttentionOps.cpp:73-320;
+  - prefill over a cached prefix with and without the key split, :2308-2507;
+  - causal prefill with the fused cache write, :649-842 and :2513-2532;
+  - chunked and recurrent DeltaNet, Qwen35HybridTextBackend.cpp:1729-1780;
+  - paged decode (bit-exact against the contiguous decode of the same rows).
+Attention outputs within max relative error 1e-2, DeltaNet states within
+1e-3; cache rows and pool pages past the attended range hold NaN."""
 import numpy as np
 import pytest
 
@@ -34,7 +37,7 @@ def _relerr(a, r):
 def _decode_cases():
     rng = np.random.default_rng(0x5EE9)
     cases = []
-    for i in range(8):
+    for i in range(16):
         D = int(rng.choice([64, 128, 256]))
         G = int(rng.choice([1, 2, 4, 8]))
         Hkv = int(rng.choice([1, 2, 4]))
@@ -75,7 +78,7 @@ def test_sweep_decode_device_lengths(i, D, G, Hkv, B, bound, lens):
 def _prefill_cases():
     rng = np.random.default_rng(0x5EEA)
     cases = []
-    for i in range(8):
+    for i in range(16):
         D = int(rng.choice([64, 128, 256]))
         G = int(rng.choice([1, 2, 4, 8]))
         Hkv = int(rng.choice([1, 2]))
@@ -107,3 +110,182 @@ def test_sweep_prefill_cached(i, D, G, Hkv, S, start):
         torch.cuda.synchronize()
         assert np.isfinite(got).all()
         assert _relerr(got, want) <= ATTN_TOL, ("split" if w is not None and need else "whole")
+
+
+def _prefill_uncached_cases():
+    rng = np.random.default_rng(0x5EEB)
+    cases = []
+    for i in range(12):
+        D = int(rng.choice([64, 128, 256]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        Hkv = int(rng.choice([1, 2]))
+        S = int(rng.integers(1, 700))
+        cache_pos = int(rng.integers(0, 50))
+        cases.append((i, D, G, Hkv, S, cache_pos))
+    return cases
+
+
+@pytest.mark.parametrize("i,D,G,Hkv,S,cache_pos", _prefill_uncached_cases())
+def test_sweep_prefill_with_cache_write(i, D, G, Hkv, S, cache_pos):
+    """Causal prefill (AttentionOps.cpp:649-842) with the fused cache write
+    (copy_to_cache, :2513-2532): output within tolerance, cache bit-exact."""
+    import torch
+    import aila_amd
+    Hq = Hkv * G
+    seed = 0x5F00 + i
+    print(f"sweep prefill {i}: D={D} G={G} Hkv={Hkv} S={S} cache_pos={cache_pos}", flush=True)
+    q = dg.normal_bf16(seed, 0, (S, Hq * D))
+    k = dg.normal_bf16(seed, 1, (S, Hkv * D))
+    v = dg.normal_bf16(seed, 2, (S, Hkv * D))
+    max_seq = cache_pos + S + 3
+    kc = torch.full((Hkv, max_seq, D), 5.0, dtype=torch.bfloat16, device="cuda")
+    vc = torch.full((Hkv, max_seq, D), 5.0, dtype=torch.bfloat16, device="cuda")
+    out = aila_amd.gqa_prefill(_t(q), _t(k), _t(v), Hq, Hkv, k_cache=kc, v_cache=vc, cache_pos=cache_pos)
+    torch.cuda.synchronize()
+    got = dg.bf16_to_f32(_np(out))
+    want = dg.bf16_to_f32(oracle.attention_prefill_naive(q, k, v, S, Hq, Hkv, D))
+    assert np.isfinite(got).all()
+    assert _relerr(got, want) <= ATTN_TOL
+    ck = np.full((Hkv, max_seq, D), dg.f32_to_bf16(np.float32([5.0]))[0], np.uint16)
+    cv = ck.copy()
+    oracle.copy_to_cache(k, ck, S, cache_pos, Hkv, D, max_seq)
+    oracle.copy_to_cache(v, cv, S, cache_pos, Hkv, D, max_seq)
+    assert np.array_equal(_np(kc), ck) and np.array_equal(_np(vc), cv)
+
+
+def _deltanet_prefill_cases():
+    rng = np.random.default_rng(0x5EEC)
+    cases = []
+    for i in range(12):
+        B = int(rng.integers(1, 4))
+        T = int(rng.integers(1, 400))
+        Hk = int(rng.choice([1, 2, 4]))
+        ratio = int(rng.choice([1, 2, 4]))
+        gates = bool(rng.integers(0, 2))
+        s0 = float(rng.choice([0.0, 0.02]))
+        cases.append((i, B, T, Hk, Hk * ratio, gates, s0))
+    return cases
+
+
+@pytest.mark.parametrize("i,B,T,Hk,Hv,gates,s0", _deltanet_prefill_cases())
+def test_sweep_deltanet_prefill(i, B, T, Hk, Hv, gates, s0):
+    """Chunked prefill against the sequential recurrence
+    (Qwen35HybridTextBackend.cpp:1729-1780): outputs 1e-2, state 1e-3."""
+    import torch
+    import aila_amd
+    d = 128
+    seed = 0x5F10 + i
+    print(f"sweep deltanet prefill {i}: B={B} T={T} Hk={Hk} Hv={Hv} gates={gates} s0={s0}", flush=True)
+    q = dg.normal_bf16(seed, 0, (B, T, Hk, d))
+    k = dg.normal_bf16(seed, 1, (B, T, Hk, d))
+    v = dg.normal_bf16(seed, 2, (B, T, Hv, d))
+    a = dg.normal_bf16(seed, 3, (B, T, Hv))
+    b = dg.normal_bf16(seed, 4, (B, T, Hv))
+    S0 = (dg.normal(seed, 5, B * Hv * d * d, std=s0).reshape(B, Hv, d, d) if s0 > 0
+          else np.zeros((B, Hv, d, d), np.float32)).astype(np.float32)
+    dtb = dg.normal_bf16(seed, 6, (Hv,), std=0.5) if gates else None
+    alog = dg.normal(seed, 7, Hv, std=0.3).astype(np.float32) if gates else None
+    st = _t(S0)
+    out = aila_amd.deltanet_prefill(_t(q), _t(k), _t(v), _t(a), _t(b), st,
+                                    dt_bias=_t(dtb) if gates else None, A_log=_t(alog) if gates else None)
+    torch.cuda.synchronize()
+    _, want_ob, want_S = oracle.deltanet_recurrent(q, k, v, a, b, S0, B, T, Hk, Hv, d, d, dt_bias=dtb, A_log=alog)
+    got_o, got_S = dg.bf16_to_f32(_np(out)), st.cpu().numpy()
+    assert np.isfinite(got_o).all() and np.isfinite(got_S).all()
+    assert _relerr(got_o, dg.bf16_to_f32(want_ob)) <= ATTN_TOL
+    assert _relerr(got_S, want_S) <= 1e-3
+
+
+def _deltanet_decode_cases():
+    rng = np.random.default_rng(0x5EED)
+    cases = []
+    for i in range(12):
+        dk = int(rng.choice([64, 128, 256]))
+        dv = int(rng.choice([64, 128, 200, 256]))
+        Hk = int(rng.choice([1, 2, 8, 16]))
+        Hv = Hk * int(rng.choice([1, 2]))
+        B = int(rng.choice([1, 3, 16, 40]))    # both sides of the wide-slab threshold
+        cases.append((i, B, Hk, Hv, dk, dv))
+    return cases
+
+
+@pytest.mark.parametrize("i,B,Hk,Hv,dk,dv", _deltanet_decode_cases())
+def test_sweep_deltanet_decode(i, B, Hk, Hv, dk, dv):
+    """Recurrent decode steps (Qwen35HybridTextBackend.cpp:1094-1148) against
+    the sequential oracle over 4 steps."""
+    import torch
+    import aila_amd
+    T = 4
+    seed = 0x5F20 + i
+    print(f"sweep deltanet decode {i}: B={B} Hk={Hk} Hv={Hv} dk={dk} dv={dv}", flush=True)
+    q = dg.normal_bf16(seed, 0, (B, T, Hk, dk))
+    k = dg.normal_bf16(seed, 1, (B, T, Hk, dk))
+    v = dg.normal_bf16(seed, 2, (B, T, Hv, dv))
+    a = dg.normal_bf16(seed, 3, (B, T, Hv))
+    b = dg.normal_bf16(seed, 4, (B, T, Hv))
+    S0 = dg.normal(seed, 5, B * Hv * dk * dv, std=0.02).reshape(B, Hv, dk, dv).astype(np.float32)
+    st = _t(S0)
+    dq, dkk, dvv, da, db = (_t(np.ascontiguousarray(x)) for x in (q, k, v, a, b))
+    outs = [aila_amd.deltanet_decode(dq[:, t].contiguous(), dkk[:, t].contiguous(), dvv[:, t].contiguous(),
+                                     da[:, t].contiguous(), db[:, t].contiguous(), st) for t in range(T)]
+    torch.cuda.synchronize()
+    got_o = dg.bf16_to_f32(np.stack([_np(o) for o in outs], axis=1))
+    _, want_ob, want_S = oracle.deltanet_recurrent(q, k, v, a, b, S0, B, T, Hk, Hv, dk, dv)
+    assert _relerr(st.cpu().numpy(), want_S) <= 1e-3
+    assert _relerr(got_o, dg.bf16_to_f32(want_ob)) <= ATTN_TOL
+
+
+def _paged_cases():
+    rng = np.random.default_rng(0x5EEE)
+    cases = []
+    for i in range(12):
+        page = int(rng.choice([16, 32, 48, 64, 128, 256]))
+        D = int(rng.choice([64, 128, 256]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        B = int(rng.integers(1, 5))
+        max_pages = int(rng.integers(2, 12))
+        lens = [int(x) for x in rng.integers(1, page * max_pages + 1, size=B)]
+        cases.append((i, page, D, G, B, max_pages, lens))
+    return cases
+
+
+@pytest.mark.parametrize("i,page,D,G,B,max_pages,lens", _paged_cases())
+def test_sweep_paged_decode(i, page, D, G, B, max_pages, lens):
+    """Paged decode equals the contiguous decode of the same rows bit for
+    bit and the oracle within tolerance; unowned pool pages hold NaN."""
+    import torch
+    import aila_amd
+    Hkv = 2
+    Hq = Hkv * G
+    max_seq = page * max_pages
+    seed = 0x5F30 + i
+    print(f"sweep paged {i}: page={page} D={D} G={G} B={B} max_pages={max_pages} lens={lens}", flush=True)
+    q = dg.normal_bf16(seed, 0, (B, Hq, D))
+    kc = dg.normal_bf16(seed, 1, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 2, (B, Hkv, max_seq, D))
+    for b, L in enumerate(lens):
+        kc[b, :, L:] = 0x7FC0
+        vc[b, :, L:] = 0x7FC0
+    npages = B * max_pages + 3
+    perm = np.random.default_rng(seed).permutation(npages)
+    pk = np.full((npages, Hkv, page, D), 0x7FC0, np.uint16)
+    pv = pk.copy()
+    table = np.zeros((B, max_pages), np.int32)
+    for b in range(B):
+        for j in range(max_pages):
+            p = int(perm[b * max_pages + j])
+            table[b, j] = p
+            pk[p] = kc[b, :, j * page:(j + 1) * page]
+            pv[p] = vc[b, :, j * page:(j + 1) * page]
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    dq = _t(q)
+    got = aila_amd.gqa_decode_paged(dq, _t(pk), _t(pv), _t(table), sl, max_seq, workspace=ws)
+    ref = aila_amd.gqa_decode(dq, _t(kc), _t(vc), max_seq, workspace=ws.clone(), seq_lens=sl)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    g = dg.bf16_to_f32(_np(got))
+    for b, L in enumerate(lens):
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(q[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv,
+                                                               D, max_seq, L))[0]
+        assert _relerr(g[b], want) <= ATTN_TOL, (b, L)
