@@ -25,8 +25,8 @@ namespace aila {
 
 // Chunked prefill of the recurrence (deltanet_prefill.hip).
 size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split);
-void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* k_lo, const bf16* v_lo,
-                             const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
+void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* q_lo, const bf16* k_lo,
+                             const bf16* v_lo, const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
                              float* state, bf16* out, unsigned char* records, int B, int T, int Hk, int Hv,
                              float eps, float scale, hipStream_t st);
 
@@ -370,8 +370,8 @@ bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) %
 // else 4; never straddling the q/k/v boundaries, all multiples of 8) over
 // kConvTok consecutive tokens, with the three previous raw rows in
 // registers. History before token 0 is the ring: h(-3) = ring[head],
-// h(-2) = ring[head+1], h(-1) = ring[head+2]. Outputs: q as bf16; k and v
-// as bf16 hi and bf16 residual lo planes, so that hi + lo carries the fp32
+// h(-2) = ring[head+1], h(-1) = ring[head+2]. Outputs: q, k and v as bf16
+// hi and bf16 residual lo planes, so that hi + lo carries the fp32
 // activation to 2^-16 relative. The first token block also writes the new
 // ring (the last three raw rows, oldest at row (head + T) % 3): it is the
 // only block that reads or writes the ring.
@@ -395,8 +395,8 @@ __device__ __forceinline__ void unpack_bf16(const typename ConvVec<CPT>::raw& r,
 template <int CPT>
 __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
     const bf16* __restrict__ qkv, int qkv_stride, const bf16* __restrict__ conv_w, float* __restrict__ conv_state,
-    int conv_head, bf16* __restrict__ q_hi, bf16* __restrict__ k_hi, bf16* __restrict__ k_lo,
-    bf16* __restrict__ v_hi, bf16* __restrict__ v_lo, int T, int qd, int vd) {
+    int conv_head, bf16* __restrict__ q_hi, bf16* __restrict__ q_lo, bf16* __restrict__ k_hi,
+    bf16* __restrict__ k_lo, bf16* __restrict__ v_hi, bf16* __restrict__ v_lo, int T, int qd, int vd) {
   using Raw = typename ConvVec<CPT>::raw;
   constexpr int NW = CPT / 2;          // 32-bit words per CPT bf16
   const int ch = 2 * qd + vd;
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
   const int width = (c < 2 * qd) ? qd : vd;
   const int col = is_q ? c : (is_k ? c - qd : c - 2 * qd);
   bf16* hi_plane = is_q ? q_hi : (is_k ? k_hi : v_hi);
-  bf16* lo_plane = is_k ? k_lo : v_lo;
+  bf16* lo_plane = is_q ? q_lo : (is_k ? k_lo : v_lo);
   // the ring after T tokens (raw rows T-3, T-2, T-1), read before the loop
   // writes nothing the block needs: only the first token block writes it
   float nr[kRows][CPT];
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
       if constexpr (CPT == 8) hw = u32x4{hp[0], hp[1], hp[2], hp[3]};
       else hw = uint2{hp[0], hp[1]};
       *reinterpret_cast<Raw*>(hi_plane + o) = hw;
-      if (!is_q) {
+      {
         float r[CPT];
 #pragma unroll
         for (int i = 0; i < CPT; ++i)
@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256) void deltanet_gate_kernel(bf16* __restrict__ o
 }
 
 struct LayerWs {   // byte offsets of the prefill workspace regions
-  size_t q_hi, k_hi, k_lo, v_hi, v_lo, records, total;
+  size_t q_hi, q_lo, k_hi, k_lo, v_hi, v_lo, records, total;
 };
 
 LayerWs layer_ws(int B, int T, int Hk, int Hv) {
@@ -570,7 +570,8 @@ LayerWs layer_ws(int B, int T, int Hk, int Hv) {
   const size_t qk = static_cast<size_t>(B) * T * Hk * kD * 2, vv = static_cast<size_t>(B) * T * Hv * kD * 2;
   LayerWs w;
   w.q_hi = 0;
-  w.k_hi = up(w.q_hi + qk);
+  w.q_lo = up(w.q_hi + qk);
+  w.k_hi = up(w.q_lo + qk);
   w.k_lo = up(w.k_hi + qk);
   w.v_hi = up(w.k_lo + qk);
   w.v_lo = up(w.v_hi + vv);
@@ -623,14 +624,14 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
     const dim3 cgrid((ch / 8 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
     hipLaunchKernelGGL(deltanet_conv_split_kernel<8>, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv),
                        qkv_stride, static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi),
-                       plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
+                       plane(w.q_lo), plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
   } else {
     const dim3 cgrid((ch / 4 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
     hipLaunchKernelGGL(deltanet_conv_split_kernel<4>, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv),
                        qkv_stride, static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi),
-                       plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
+                       plane(w.q_lo), plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
   }
-  launch_deltanet_chunked(plane(w.q_hi), plane(w.k_hi), plane(w.v_hi), plane(w.k_lo), plane(w.v_lo),
+  launch_deltanet_chunked(plane(w.q_hi), plane(w.k_hi), plane(w.v_hi), plane(w.q_lo), plane(w.k_lo), plane(w.v_lo),
                           static_cast<const bf16*>(a), static_cast<const bf16*>(b), ab_stride,
                           static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out), ws + w.records,
                           B, T, Hk, Hv, eps, scale, st);

@@ -93,14 +93,18 @@ struct ChunkRec {
 
 // ---------------------------------------------------------------------------
 // kLo: the inputs are fp32 values carried as bf16 hi planes (q, k, v) plus
-// bf16 residual planes (k_lo, v_lo). The residuals enter exactly where the
-// rounding of an input would reach the state beyond fp32 accuracy: the key
-// norms, U (its MFMA pass and diagonal term) and the K^T operand of the
-// state update (a KtLo record); K K^T, W, P and Q use the hi planes.
+// bf16 residual planes (q_lo, k_lo, v_lo). The residuals enter exactly where
+// the rounding of an input would reach the state beyond fp32 accuracy - the
+// key norms, U (its MFMA pass and diagonal term) and the K^T operand of the
+// state update (a KtLo record) - and where it would reach the outputs of
+// rows whose q.k nearly cancels (the gated RMSNorm after the layer then
+// magnifies an output far below sqrt(eps)): P = Q K^T takes Q_hi K_hi +
+// Q_hi K_lo + Q_lo K_hi and the scan's Q S takes S as hi + lo. K K^T and W
+// use the hi planes.
 template <int DK, int DV, bool kLo>
 __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const bf16* __restrict__ k_lo, const bf16* __restrict__ v_lo,
+    const bf16* __restrict__ q_lo, const bf16* __restrict__ k_lo, const bf16* __restrict__ v_lo,
     const bf16* __restrict__ a, const bf16* __restrict__ bg, int ab_stride, const bf16* __restrict__ dt_bias,
     const float* __restrict__ A_log, unsigned char* __restrict__ ws, int T, int Hk, int Hv,
     float eps) {
@@ -132,6 +136,11 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const u32x4 rk = buffer_rsrc(k + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
     const u32x4 rq = buffer_rsrc(q + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
     const u32x4 rv = buffer_rsrc(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV, (n - 1) * v_row + RB);
+    // split inputs: the query residual takes the V buffer until P is formed
+    // (V is first read by U, after the inverse, and arrives meanwhile)
+    const u32x4 rql = kLo ? buffer_rsrc(q_lo + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK,
+                                        (n - 1) * kq_row + RB)
+                          : rv;
 #pragma unroll
     for (int i = 0; i < kC * NC / kThreads; ++i) {
       const int slot = i * 4 + wave;                       // wave-contiguous KiB
@@ -139,7 +148,8 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int r = p / NC, cc = p % NC;
       dma16_to_lds(rk, r * kq_row + ((cc ^ swz_rows(r)) << 4), sK + slot * 1024);
       dma16_to_lds(rq, r * kq_row + ((cc ^ swz_rows(r)) << 4), sQA + slot * 1024);
-      dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
+      if constexpr (kLo) dma16_to_lds(rql, r * kq_row + ((cc ^ swz_rows(r)) << 4), sVW + slot * 1024);
+      else dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
     }
     if constexpr (kLo) {
       // key residual tile into the To buffer, which is free until step 4
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const int r = tid >> 2, part = tid & 3;
     float sk = 0.f, sq = 0.f;
     if constexpr (kLo) {
-      // |k|^2 of the fp32 key hi + lo
+      // |k|^2 and |q|^2 of the fp32 key and query, hi + lo
       float hi[8], lo[8];
 #pragma unroll
       for (int cc = 0; cc < NC / 4; ++cc) {
@@ -195,6 +205,13 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
           const float x = r < n ? hi[e] + lo[e] : 0.f;
           sk = fmaf(x, x, sk);
         }
+        unpack8(row_chunk(sQA, r, part * (NC / 4) + cc), hi);
+        unpack8(row_chunk(sVW, r, part * (NC / 4) + cc), lo);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = hi[e] + lo[e];
+          sq = fmaf(x, x, sq);
+        }
       }
     }
 #pragma unroll
@@ -204,8 +221,10 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       unpack8(row_chunk(sQA, r, part * (NC / 4) + cc), qf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        if constexpr (!kLo) sk = fmaf(kf[e], kf[e], sk);
-        sq = fmaf(qf[e], qf[e], sq);
+        if constexpr (!kLo) {
+          sk = fmaf(kf[e], kf[e], sk);
+          sq = fmaf(qf[e], qf[e], sq);
+        }
       }
     }
     sk += __shfl_xor(sk, 1);
@@ -230,8 +249,10 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int l = o & 63, ks = (o >> 6) & 3, tw = o >> 8;
       const int r = tw * 16 + (l & 15), g = l >> 4;
       const int k0 = ks * 32 + 4 * g, k1 = k0 + 16;   // slots 0..3 and 4..7
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(sQA + r * RB + (((k0 >> 3) ^ swz_rows(r)) << 4) + ((k0 & 7) << 1));
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(sQA + r * RB + (((k1 >> 3) ^ swz_rows(r)) << 4) + ((k1 & 7) << 1));
+      const int a0 = r * RB + (((k0 >> 3) ^ swz_rows(r)) << 4) + ((k0 & 7) << 1);
+      const int a1 = r * RB + (((k1 >> 3) ^ swz_rows(r)) << 4) + ((k1 & 7) << 1);
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(sQA + a0);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(sQA + a1);
       Qout[o] = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
   }
@@ -268,14 +289,34 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
         const int tj = 2 * s2 + h;
         if (tj <= ti) {
 #pragma unroll
-          for (int ks = 0; ks < DK / 32; ++ks)
-            acc3[i][h] = mfma16x16x32(as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4)),
-                                      as_bf16x8(row_chunk(sQA, ti * 16 + m16, ks * 4 + g4)), acc3[i][h]);
+          for (int ks = 0; ks < DK / 32; ++ks) {
+            const bf16x8_t kb = as_bf16x8(row_chunk(sK, tj * 16 + m16, ks * 4 + g4));
+            const bf16x8_t qb = as_bf16x8(row_chunk(sQA, ti * 16 + m16, ks * 4 + g4));
+            acc3[i][h] = mfma16x16x32(kb, qb, acc3[i][h]);
+            if constexpr (kLo) {
+              // split inputs: the rounding of q and k would otherwise reach
+              // the outputs of rows whose q.k nearly cancels
+              acc3[i][h] = mfma16x16x32(as_bf16x8(row_chunk(sKl, tj * 16 + m16, ks * 4 + g4)), qb, acc3[i][h]);
+              acc3[i][h] = mfma16x16x32(kb, as_bf16x8(row_chunk(sVW, ti * 16 + m16, ks * 4 + g4)), acc3[i][h]);
+            }
+          }
         }
       }
     }
   }
   __syncthreads();   // Q is no longer read: its space becomes A
+  if constexpr (kLo) {
+    // the query residual is spent: V into its buffer, waited for with V_lo
+    const int v_row = Hv * DV * 2;
+    const u32x4 rv = buffer_rsrc(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV, (n - 1) * v_row + RB);
+#pragma unroll
+    for (int i = 0; i < kC * NC / kThreads; ++i) {
+      const int slot = i * 4 + wave;
+      const int p = slot * 64 + lane;
+      const int r = p / NC, cc = p % NC;
+      dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
+    }
+  }
   auto v4 = [&](const float* arr, int i0) __attribute__((always_inline)) { return *reinterpret_cast<const f32x4*>(arr + i0); };
   u32x4* Pout = reinterpret_cast<u32x4*>(rec + R::kP);
 #pragma unroll
@@ -736,7 +777,13 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       if (active) {
 #pragma unroll
-        for (int ks = 0; ks < DK / 32; ++ks) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sS[ks][lane]), acc);
+        for (int ks = 0; ks < DK / 32; ++ks) {
+          const bf16x8_t sh = as_bf16x8(sS[ks][lane]);
+          acc = mfma16x16x32(as_bf16x8(o.q[ks]), sh, acc);
+          // split inputs: S as hi + lo (the residual of Q adds ~15% to the
+          // scan's operand bytes for no measurable gain: P carries it)
+          if constexpr (kLo) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sSl[ks][lane]), acc);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] *= o.fq[j];
       }
@@ -779,19 +826,20 @@ size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split) {
   return static_cast<size_t>(B) * Hv * nch * (split ? ChunkRec<128, 128, true>::kBytes : ChunkRec<128, 128, false>::kBytes);
 }
 
-void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* k_lo, const bf16* v_lo,
+void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* q_lo, const bf16* k_lo,
+                             const bf16* v_lo,
                              const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
                              float* state, bf16* out, unsigned char* records, int B, int T, int Hk, int Hv,
                              float eps, float scale, hipStream_t st) {
   const int nch = (T + kC - 1) / kC;
   if (k_lo) {
     hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128, true>), dim3(nch, Hv, B), dim3(kThreads), 0, st, q, k,
-                       v, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
+                       v, q_lo, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
     hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128, true>), dim3(128 / 16, Hv, B), dim3(2 * kThreads), 0,
                        st, q, records, state, out, T, Hk, Hv, scale);
   } else {
     hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128, false>), dim3(nch, Hv, B), dim3(kThreads), 0, st, q, k,
-                       v, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
+                       v, q_lo, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
     hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128, false>), dim3(128 / 16, Hv, B), dim3(2 * kThreads), 0,
                        st, q, records, state, out, T, Hk, Hv, scale);
   }
@@ -818,7 +866,7 @@ extern "C" int aila_hip_deltanet_prefill(const void* q, const void* k, const voi
   if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_prefill: workspace %zu < %zu bytes", workspace_bytes, need);
   launch_deltanet_chunked(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                          nullptr, nullptr, static_cast<const bf16*>(a), static_cast<const bf16*>(b), Hv,
+                          nullptr, nullptr, nullptr, static_cast<const bf16*>(a), static_cast<const bf16*>(b), Hv,
                           static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out),
                           static_cast<unsigned char*>(workspace), B, T, Hk, Hv, eps, scale,
                           static_cast<hipStream_t>(stream));
