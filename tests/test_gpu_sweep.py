@@ -5,7 +5,9 @@ not pin one by one, each case checked against the CPU oracle:
   - prefill over a cached prefix with and without the key split, :2308-2507;
   - causal prefill with the fused cache write, :649-842 and :2513-2532;
   - chunked and recurrent DeltaNet, Qwen35HybridTextBackend.cpp:1729-1780;
-  - paged decode (bit-exact against the contiguous decode of the same rows).
+  - paged decode (bit-exact against the contiguous decode of the same rows);
+  - the fused decode preparation + append + decode at device positions;
+  - the whole DeltaNet layer, prefill then decode steps.
 Attention outputs within max relative error 1e-2, DeltaNet states within
 1e-3; cache rows and pool pages past the attended range hold NaN."""
 import numpy as np
@@ -289,3 +291,121 @@ def test_sweep_paged_decode(i, page, D, G, B, max_pages, lens):
         want = dg.bf16_to_f32(oracle.attention_decode_baseline(q[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv,
                                                                D, max_seq, L))[0]
         assert _relerr(g[b], want) <= ATTN_TOL, (b, L)
+
+
+def _fused_prep_cases():
+    rng = np.random.default_rng(0x5EEF)
+    cases = []
+    for i in range(10):
+        D = int(rng.choice([64, 128, 256]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        Hkv = int(rng.choice([1, 2, 4]))
+        B = int(rng.integers(1, 5))
+        rot = int(rng.choice([32, 64, D]))
+        packed = bool(rng.integers(0, 2))
+        split = bool(rng.integers(0, 2))
+        max_seq = int(rng.integers(64, 2500))
+        pos = [int(x) for x in rng.integers(0, max_seq, size=B)]
+        cases.append((i, D, G, Hkv, B, rot, packed, split, max_seq, pos))
+    return cases
+
+
+@pytest.mark.parametrize("i,D,G,Hkv,B,rot,packed,split,max_seq,pos", _fused_prep_cases())
+def test_sweep_fused_prepare_append_decode(i, D, G, Hkv, B, rot, packed, split, max_seq, pos):
+    """One launch of QK-norm + RoPE + K/V append + decode at device positions
+    (decode_prepare_qkv, ElementwiseOps.cpp:105-216, then attention_decode)
+    against the oracle's prep followed by its attention."""
+    import torch
+    import aila_amd
+    Hq = Hkv * G
+    seed, theta, eps = 0x5F40 + i, 1e6, 1e-6
+    print(f"sweep fused prep {i}: D={D} G={G} Hkv={Hkv} B={B} rot={rot} packed={packed} split={split} "
+          f"max_seq={max_seq} pos={pos}", flush=True)
+    posa = np.array(pos, np.int32)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D if packed else D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
+    for b, p in enumerate(pos):      # rows past the appended one are never attended
+        kc[b, :, p + 1:] = 0x7FC0
+        vc[b, :, p + 1:] = 0x7FC0
+    kc_d, vc_d = _t(kc), _t(vc)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda") if split else None
+    res = aila_amd.gqa_decode_prepare_append(
+        _t(q), _t(k), _t(v), kc_d, vc_d, max_seq - 1, q_norm_w=_t(qw), k_norm_w=_t(kw), rotary_dim=rot,
+        theta=theta, eps=eps, packed_gate=packed, positions=_t(posa), workspace=ws)
+    torch.cuda.synchronize()
+    out = res[0] if packed else res
+    qo, gw, ko = oracle.decode_prepare(q, k, v, qw, kw, kc, vc, posa, B, Hq, Hkv, D, max_seq, rot, theta, eps,
+                                       packed=packed)
+    got = dg.bf16_to_f32(_np(out))
+    assert np.isfinite(got).all()
+    for b in range(B):
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(qo[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv,
+                                                               D, max_seq, pos[b] + 1))[0]
+        assert _relerr(got[b], want) <= ATTN_TOL, f"sequence {b}"
+    if packed:
+        assert np.array_equal(_np(res[1]), gw)
+
+
+def _layer_cases():
+    rng = np.random.default_rng(0x5EF1)
+    cases = []
+    for i in range(8):
+        B = int(rng.integers(1, 4))
+        Hk = int(rng.choice([1, 2, 4]))
+        Hv = Hk * int(rng.choice([1, 2, 4]))
+        T = int(rng.integers(1, 300))
+        steps = int(rng.integers(1, 5))
+        head0 = int(rng.integers(0, 3))
+        wide = bool(rng.integers(0, 2))
+        cases.append((i, B, Hk, Hv, T, steps, head0, wide))
+    return cases
+
+
+@pytest.mark.parametrize("i,B,Hk,Hv,T,steps,head0,wide", _layer_cases())
+def test_sweep_layer_prefill_then_decode(i, B, Hk, Hv, T, steps, head0, wide):
+    """Whole DeltaNet layer (conv ring + SiLU, L2 norms, recurrence, gated
+    RMSNorm; Qwen35HybridTextBackend.cpp:1640-1798): a T-token prefill, then
+    decode steps, against the oracle's layer over all T + steps tokens.
+    State 1e-3, outputs 1e-2, conv ring bit-exact."""
+    import torch
+    import aila_amd
+    d = 128
+    seed = 0x5F50 + i
+    total = T + steps
+    print(f"sweep layer {i}: B={B} Hk={Hk} Hv={Hv} T={T} steps={steps} head0={head0} wide={wide}", flush=True)
+    ch = 2 * Hk * d + Hv * d
+    qkv = dg.normal_bf16(seed, 0, (B, total, ch))
+    z = dg.normal_bf16(seed, 1, (B, total, Hv * d))
+    a = dg.normal_bf16(seed, 2, (B, total, Hv))
+    b = dg.normal_bf16(seed, 3, (B, total, Hv))
+    conv_w = dg.normal_bf16(seed, 4, (ch, 4), std=0.5)
+    conv_state = dg.normal(seed, 5, B * 3 * ch).reshape(B, 3, ch).astype(np.float32)
+    norm_w = (1.0 + dg.normal(seed, 6, d, std=0.1)).astype(np.float32)
+    S0 = dg.normal(seed, 7, B * Hv * d * d, std=0.02).reshape(B, Hv, d, d).astype(np.float32)
+    dtb = dg.normal_bf16(seed, 8, (Hv,))
+    alog = np.log(1.0 + np.abs(dg.normal(seed, 9, Hv, std=4.0))).astype(np.float32)
+    want_out, want_S, want_cs = oracle.deltanet_layer(qkv, z, a, b, conv_w, conv_state, head0, norm_w, S0, B,
+                                                      total, Hk, Hv, d, d, dt_bias=dtb, A_log=alog, fast=True)
+    st, cs = _t(S0), _t(conv_state)
+    w, nw, dtb_d, alog_d = _t(conv_w), _t(norm_w), _t(dtb), _t(alog)
+    dqkv, dz, da, db = _t(qkv), _t(z), _t(a), _t(b)
+    outs = [aila_amd.deltanet_layer_prefill(dqkv[:, :T].contiguous(), dz[:, :T].contiguous(),
+                                            da[:, :T].contiguous(), db[:, :T].contiguous(), w, cs, head0, nw, st,
+                                            Hk, dt_bias=dtb_d, A_log=alog_d)]
+    arr = torch.zeros(B * Hk, dtype=torch.int32, device="cuda") if wide else None
+    for t in range(T, total):
+        o = aila_amd.deltanet_layer_decode(dqkv[:, t], dz[:, t], da[:, t], db[:, t], w, cs, (head0 + t) % 3, nw,
+                                           st, Hk, dt_bias=dtb_d, A_log=alog_d, arrivals=arr)
+        outs.append(o.view(B, 1, Hv * d))
+    torch.cuda.synchronize()
+    got_out = dg.bf16_to_f32(np.concatenate([_np(o).reshape(B, -1, Hv * d) for o in outs], axis=1))
+    assert _relerr(st.cpu().numpy(), want_S) <= 1e-3
+    assert _relerr(got_out, dg.bf16_to_f32(want_out).reshape(B, total, Hv * d)) <= ATTN_TOL
+    assert np.array_equal(cs.cpu().numpy(), want_cs)
+    if wide:
+        assert not arr.any()
