@@ -202,6 +202,18 @@ __device__ __forceinline__ u32x2 ds_read_tr4(const void* lds_addr) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// Layer prefill input of the DeltaNet chunk prep: the chunk's q, k, v are
+// the causal conv1d (4 taps) + SiLU of fused [q | k | v | ...] token rows,
+// formed by the prep itself.
+struct ConvIn {
+  const bf16* qkv;     // [B, T, stride] bf16
+  int stride;          // elements per token row
+  const bf16* w;       // [ch, 4] taps
+  const float* ring;   // [B, 3, ch] fp32 raw rows before token 0
+  int head;            // ring row holding token -3 (mod 3)
+  int ch;              // channels of a row's [q | k | v] part
+};
+
 }  // namespace aila
 
 // ---- host-side error plumbing (defined in capi.hip) ---------------------

@@ -25,10 +25,11 @@ namespace aila {
 
 // Chunked prefill of the recurrence (deltanet_prefill.hip).
 size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split);
-void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* q_lo, const bf16* k_lo,
-                             const bf16* v_lo, const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
-                             float* state, bf16* out, unsigned char* records, int B, int T, int Hk, int Hv,
-                             float eps, float scale, hipStream_t st);
+// conv == nullptr: q, k, v planes; else the layer (q, k, v formed from conv->qkv).
+void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const ConvIn* conv, const bf16* a,
+                             const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log, float* state,
+                             bf16* out, unsigned char* records, int B, int T, int Hk, int Hv, float eps, float scale,
+                             hipStream_t st);
 
 namespace {
 
@@ -365,168 +366,31 @@ __global__ __launch_bounds__(NT) void deltanet_layer_decode_vh_kernel(
 
 bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
-// ---- prefill: causal conv + SiLU over T tokens into split planes ----------
-// Thread = CPT consecutive channels (8 when the rows allow 16-byte access,
-// else 4; never straddling the q/k/v boundaries, all multiples of 8) over
-// kConvTok consecutive tokens, with the three previous raw rows in
-// registers. History before token 0 is the ring: h(-3) = ring[head],
-// h(-2) = ring[head+1], h(-1) = ring[head+2]. Outputs: q, k and v as bf16
-// hi and bf16 residual lo planes, so that hi + lo carries the fp32
-// activation to 2^-16 relative. The first token block also writes the new
-// ring (the last three raw rows, oldest at row (head + T) % 3): it is the
-// only block that reads or writes the ring.
-constexpr int kConvTok = 16;    // (32 and 64 measured 1-3% slower at the config-4 shape)
-constexpr int kConvBatch = 8;   // rows loaded together before they are used
-
-template <int CPT>
-struct ConvVec;
-template <>
-struct ConvVec<4> { using raw = uint2; };
-template <>
-struct ConvVec<8> { using raw = u32x4; };
-
-template <int CPT>
-__device__ __forceinline__ void unpack_bf16(const typename ConvVec<CPT>::raw& r, float (&x)[CPT]) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(&r);
-#pragma unroll
-  for (int i = 0; i < CPT; ++i) x[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
-}
-
-template <int CPT>
-__global__ __launch_bounds__(256) void deltanet_conv_split_kernel(
-    const bf16* __restrict__ qkv, int qkv_stride, const bf16* __restrict__ conv_w, float* __restrict__ conv_state,
-    int conv_head, bf16* __restrict__ q_hi, bf16* __restrict__ q_lo, bf16* __restrict__ k_hi,
-    bf16* __restrict__ k_lo, bf16* __restrict__ v_hi, bf16* __restrict__ v_lo, int T, int qd, int vd) {
-  using Raw = typename ConvVec<CPT>::raw;
-  constexpr int NW = CPT / 2;          // 32-bit words per CPT bf16
-  const int ch = 2 * qd + vd;
-  const int c = (blockIdx.x * 256 + threadIdx.x) * CPT;
-  if (c >= ch) return;
-  const int b = blockIdx.z;
-  const int tb0 = blockIdx.y * kConvTok;
-  const int tend = min(T, tb0 + kConvTok);
-  const int head = ((conv_head % kRows) + kRows) % kRows;
-  const bf16* xb = qkv + static_cast<size_t>(b) * T * qkv_stride + c;
-  float* ring = conv_state + static_cast<size_t>(b) * kRows * ch + c;
-
-  // taps: w[c+i][j] for the CPT channels (CPT * 4 bf16, 16-byte loads)
-  float w[CPT][4];
-  {
-    uint32_t ww[CPT * 2];
-#pragma unroll
-    for (int v4 = 0; v4 < CPT / 2; ++v4) {   // 16 bytes = the taps of two channels
-      const u32x4 r = *reinterpret_cast<const u32x4*>(conv_w + static_cast<size_t>(c) * kConvK + v4 * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ww[v4 * 4 + e] = r[e];
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t word = ww[(i * 4 + j) >> 1];
-        w[i][j] = __uint_as_float(((i * 4 + j) & 1) ? (word & 0xffff0000u) : (word << 16));
-      }
-  }
-  // All per-row values live in plain float arrays indexed by compile-time
-  // constants (a runtime choice among local rows puts them in scratch).
-  auto load_x = [&](int t, float (&dst)[CPT]) __attribute__((always_inline)) {
-    unpack_bf16<CPT>(*reinterpret_cast<const Raw*>(xb + static_cast<size_t>(t) * qkv_stride), dst);
-  };
-  // raw row i (i >= -3) into dst: token rows from qkv, i < 0 from the ring
-  // (ring row (head + 3 + i) % 3 holds raw row i)
-  auto hist = [&](int i, float (&dst)[CPT]) __attribute__((always_inline)) {
-    if (i >= 0) {
-      load_x(i, dst);
-    } else {
-#pragma unroll
-      for (int v4 = 0; v4 < CPT / 4; ++v4) {
-        const f32x4 r = *reinterpret_cast<const f32x4*>(ring + static_cast<size_t>((head + kRows + i) % kRows) * ch + v4 * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[v4 * 4 + e] = r[e];
-      }
-    }
-  };
-  float h0[CPT], h1[CPT], h2[CPT];
-  hist(tb0 - 3, h0);
-  hist(tb0 - 2, h1);
-  hist(tb0 - 1, h2);
-  // destination plane and column
-  const bool is_q = c < qd, is_k = !is_q && c < 2 * qd;
-  const int width = (c < 2 * qd) ? qd : vd;
-  const int col = is_q ? c : (is_k ? c - qd : c - 2 * qd);
-  bf16* hi_plane = is_q ? q_hi : (is_k ? k_hi : v_hi);
-  bf16* lo_plane = is_q ? q_lo : (is_k ? k_lo : v_lo);
-  // the ring after T tokens (raw rows T-3, T-2, T-1), read before the loop
-  // writes nothing the block needs: only the first token block writes it
-  float nr[kRows][CPT];
-  if (tb0 == 0) {
-#pragma unroll
-    for (int j = 0; j < kRows; ++j) hist(T - kRows + j, nr[j]);
-  }
-  for (int tb = tb0; tb < tend; tb += kConvBatch) {
-    // a batch of rows in flight at once (clamped, so the loads stay unconditional)
-    float xs[kConvBatch][CPT];
-#pragma unroll
-    for (int i = 0; i < kConvBatch; ++i) load_x(min(tb + i, T - 1), xs[i]);
-#pragma unroll
-    for (int u = 0; u < kConvBatch; ++u) {
-      const int t = tb + u;
-      if (t >= tend) break;
-      float y[CPT];
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        float acc = h0[i] * w[i][0];
-        acc += h1[i] * w[i][1];
-        acc += h2[i] * w[i][2];
-        acc += xs[u][i] * w[i][3];
-        y[i] = silu_f(acc);
-      }
-      uint32_t hp[NW], lp[NW];
-#pragma unroll
-      for (int e = 0; e < NW; ++e) hp[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
-      const size_t o = (static_cast<size_t>(b) * T + t) * width + col;
-      Raw hw;
-      if constexpr (CPT == 8) hw = u32x4{hp[0], hp[1], hp[2], hp[3]};
-      else hw = uint2{hp[0], hp[1]};
-      *reinterpret_cast<Raw*>(hi_plane + o) = hw;
-      {
-        float r[CPT];
-#pragma unroll
-        for (int i = 0; i < CPT; ++i)
-          r[i] = y[i] - __uint_as_float((i & 1) ? (hp[i >> 1] & 0xffff0000u) : (hp[i >> 1] << 16));
-#pragma unroll
-        for (int e = 0; e < NW; ++e) lp[e] = pack_bf16x2(r[2 * e], r[2 * e + 1]);
-        Raw lw;
-        if constexpr (CPT == 8) lw = u32x4{lp[0], lp[1], lp[2], lp[3]};
-        else lw = uint2{lp[0], lp[1]};
-        *reinterpret_cast<Raw*>(lo_plane + o) = lw;
-      }
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        h0[i] = h1[i];
-        h1[i] = h2[i];
-        h2[i] = xs[u][i];
-      }
-    }
-  }
-  if (tb0 == 0) {
-    // the ring after T tokens: raw rows T-3, T-2, T-1 at rows (head + T + j) % 3
-#pragma unroll
-    for (int j = 0; j < kRows; ++j)
-#pragma unroll
-      for (int v4 = 0; v4 < CPT / 4; ++v4)
-        *reinterpret_cast<f32x4*>(ring + static_cast<size_t>((head + T + j) % kRows) * ch + v4 * 4) =
-            f32x4{nr[j][v4 * 4], nr[j][v4 * 4 + 1], nr[j][v4 * 4 + 2], nr[j][v4 * 4 + 3]};
-  }
-}
-
 // ---- prefill epilogue: out = RMSNorm(o) * norm_w * SiLU(z), in place ------
 // A (token, value head) row of 128 outputs per 16 lanes (8 per lane, one
-// 16-byte access each); kGateRows rows per 256-thread block.
+// 16-byte access each); kGateRows rows per 256-thread block. Blocks past
+// gate_blocks write the conv ring after T tokens: raw rows T-3, T-2, T-1 at
+// ring rows (head + T + j) % 3 (a row whose token would be before token 0
+// keeps its value). The chunk prep reads the old ring (tokens before 0), so
+// the ring is rewritten only after it.
 constexpr int kGateRows = 16 * 2;
 __global__ __launch_bounds__(256) void deltanet_gate_kernel(bf16* __restrict__ out, const bf16* __restrict__ z,
                                                             int z_stride, const float* __restrict__ norm_w,
-                                                            long rows, int Hv, float eps) {
+                                                            long rows, int Hv, float eps, int gate_blocks,
+                                                            const bf16* __restrict__ qkv, int qkv_stride,
+                                                            float* __restrict__ ring, int head, int T, int ch,
+                                                            int B) {
+  if (static_cast<int>(blockIdx.x) >= gate_blocks) {
+    const long i = static_cast<long>(blockIdx.x - gate_blocks) * 256 + threadIdx.x;   // over [B][3][ch]
+    if (i >= static_cast<long>(B) * kRows * ch) return;
+    const int c = static_cast<int>(i % ch), j = static_cast<int>((i / ch) % kRows);
+    const int bb = static_cast<int>(i / (static_cast<long>(kRows) * ch));
+    const int t = T - kRows + j;
+    if (t >= 0)
+      ring[(static_cast<size_t>(bb) * kRows + (head + T + j) % kRows) * ch + c] =
+          bf2f(qkv[(static_cast<size_t>(bb) * T + t) * qkv_stride + c]);
+    return;
+  }
   const int sub = threadIdx.x & 15;
   const f32x4 nw0 = *reinterpret_cast<const f32x4*>(norm_w + sub * 8);
   const f32x4 nw1 = *reinterpret_cast<const f32x4*>(norm_w + sub * 8 + 4);
@@ -561,24 +425,9 @@ __global__ __launch_bounds__(256) void deltanet_gate_kernel(bf16* __restrict__ o
   }
 }
 
-struct LayerWs {   // byte offsets of the prefill workspace regions
-  size_t q_hi, q_lo, k_hi, k_lo, v_hi, v_lo, records, total;
-};
-
-LayerWs layer_ws(int B, int T, int Hk, int Hv) {
-  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-  const size_t qk = static_cast<size_t>(B) * T * Hk * kD * 2, vv = static_cast<size_t>(B) * T * Hv * kD * 2;
-  LayerWs w;
-  w.q_hi = 0;
-  w.q_lo = up(w.q_hi + qk);
-  w.k_hi = up(w.q_lo + qk);
-  w.k_lo = up(w.k_hi + qk);
-  w.v_hi = up(w.k_lo + qk);
-  w.v_lo = up(w.v_hi + vv);
-  w.records = up(w.v_lo + vv);
-  w.total = w.records + deltanet_chunk_records_bytes(B, T, Hv, true);
-  return w;
-}
+// The prefill workspace holds the chunk records only (the prep forms q, k,
+// v from the fused rows itself).
+size_t layer_ws_bytes(int B, int T, int Hv) { return deltanet_chunk_records_bytes(B, T, Hv, true); }
 
 }  // namespace
 
@@ -586,7 +435,7 @@ LayerWs layer_ws(int B, int T, int Hk, int Hv) {
 
 extern "C" size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk, int Hv, int dk, int dv) {
   if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || dk != aila::kD || dv != aila::kD) return 0;
-  return aila::layer_ws(B, T, Hk, Hv).total;
+  return aila::layer_ws_bytes(B, T, Hv);
 }
 
 extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, const void* z, int z_stride,
@@ -612,32 +461,22 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
                    aligned(z, 16) && z_stride % 8 == 0 && aligned(norm_w, 16) && aligned(state, 16) &&
                    aligned(out, 16),
                "deltanet_layer_prefill: misaligned qkv/conv_w/conv_state/z/norm_w/state/out or odd strides");
-  const LayerWs w = layer_ws(B, T, Hk, Hv);
-  if (!workspace || workspace_bytes < w.total)
+  const size_t need = layer_ws_bytes(B, T, Hv);
+  if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_layer_prefill: workspace %zu < %zu bytes", workspace_bytes,
-                     w.total);
+                     need);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  auto plane = [&](size_t off) { return reinterpret_cast<bf16*>(ws + off); };
-  // 16-byte row access when the fused rows allow it
-  if (aligned(qkv, 16) && qkv_stride % 8 == 0) {
-    const dim3 cgrid((ch / 8 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
-    hipLaunchKernelGGL(deltanet_conv_split_kernel<8>, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv),
-                       qkv_stride, static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi),
-                       plane(w.q_lo), plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
-  } else {
-    const dim3 cgrid((ch / 4 + 255) / 256, (T + kConvTok - 1) / kConvTok, B);
-    hipLaunchKernelGGL(deltanet_conv_split_kernel<4>, cgrid, dim3(256), 0, st, static_cast<const bf16*>(qkv),
-                       qkv_stride, static_cast<const bf16*>(conv_w), conv_state, conv_head, plane(w.q_hi),
-                       plane(w.q_lo), plane(w.k_hi), plane(w.k_lo), plane(w.v_hi), plane(w.v_lo), T, qd, vd);
-  }
-  launch_deltanet_chunked(plane(w.q_hi), plane(w.k_hi), plane(w.v_hi), plane(w.q_lo), plane(w.k_lo), plane(w.v_lo),
-                          static_cast<const bf16*>(a), static_cast<const bf16*>(b), ab_stride,
-                          static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out), ws + w.records,
-                          B, T, Hk, Hv, eps, scale, st);
+  const int head = ((conv_head % kRows) + kRows) % kRows;
+  const ConvIn cv{static_cast<const bf16*>(qkv), qkv_stride, static_cast<const bf16*>(conv_w), conv_state, head, ch};
+  launch_deltanet_chunked(nullptr, nullptr, nullptr, &cv, static_cast<const bf16*>(a), static_cast<const bf16*>(b),
+                          ab_stride, static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out),
+                          static_cast<unsigned char*>(workspace), B, T, Hk, Hv, eps, scale, st);
   const long rows = static_cast<long>(B) * T * Hv;
-  hipLaunchKernelGGL(deltanet_gate_kernel, dim3(static_cast<unsigned>((rows + kGateRows - 1) / kGateRows)), dim3(256), 0, st,
-                     static_cast<bf16*>(out), static_cast<const bf16*>(z), z_stride, norm_w, rows, Hv, eps);
+  const int gate_blocks = static_cast<int>((rows + kGateRows - 1) / kGateRows);
+  const int ring_blocks = static_cast<int>((static_cast<long>(B) * kRows * ch + 255) / 256);
+  hipLaunchKernelGGL(deltanet_gate_kernel, dim3(static_cast<unsigned>(gate_blocks + ring_blocks)), dim3(256), 0, st,
+                     static_cast<bf16*>(out), static_cast<const bf16*>(z), z_stride, norm_w, rows, Hv, eps,
+                     gate_blocks, static_cast<const bf16*>(qkv), qkv_stride, conv_state, head, T, ch, B);
   return check_launch("deltanet_layer_prefill");
 }
 

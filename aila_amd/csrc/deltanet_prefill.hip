@@ -93,7 +93,8 @@ struct ChunkRec {
 
 // ---------------------------------------------------------------------------
 // kLo: the inputs are fp32 values carried as bf16 hi planes (q, k, v) plus
-// bf16 residual planes (q_lo, k_lo, v_lo). The residuals enter exactly where
+// bf16 residual tiles (q_lo, k_lo, v_lo), formed in the prep from the conv
+// of the fused rows (ConvIn). The residuals enter exactly where
 // the rounding of an input would reach the state beyond fp32 accuracy - the
 // key norms, U (its MFMA pass and diagonal term) and the K^T operand of the
 // state update (a KtLo record) - and where it would reach the outputs of
@@ -104,7 +105,7 @@ struct ChunkRec {
 template <int DK, int DV, bool kLo>
 __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const bf16* __restrict__ q_lo, const bf16* __restrict__ k_lo, const bf16* __restrict__ v_lo,
+    ConvIn cv,
     const bf16* __restrict__ a, const bf16* __restrict__ bg, int ab_stride, const bf16* __restrict__ dt_bias,
     const float* __restrict__ A_log, unsigned char* __restrict__ ws, int T, int Hk, int Hv,
     float eps) {
@@ -130,17 +131,114 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   const int m16 = lane & 15, g4 = lane >> 4;
   unsigned char* rec = ws + ((static_cast<size_t>(b) * Hv + hv) * nch + c) * R::kBytes;
 
-  // ---- 1. K, Q, V tiles by DMA (rows past T read as zeros) --------------------
-  {
+  // ---- 1. K, Q, V tiles (rows past T are zero) ---------------------------------
+  // Split inputs (the layer): thread (cc, r0) forms 16-byte chunk cc of rows
+  // r0 .. r0+3 of each tile: conv of the 7 raw rows r0-3 .. r0+3 (rows
+  // before token 0 from the ring), SiLU, then bf16 hi and residual. Q, K and
+  // the K residual go to their tiles now; V, its residual and a second copy
+  // of the K residual wait in registers for buffers that free up later.
+  const int cc1 = tid & 15, r01 = (tid >> 4) * 4;
+  u32x4 vh1[4], vl1[4], kl1[4];
+  auto put_rows = [&](unsigned char* tile, bool trswz, const u32x4 (&x)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r01 + i;
+      *reinterpret_cast<u32x4*>(tile + r * RB + ((cc1 ^ (trswz ? swz_tr(r) : swz_rows(r))) << 4)) = x[i];
+    }
+  };
+  if constexpr (kLo) {
+    const int head = ((cv.head % 3) + 3) % 3;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(cv.qkv + static_cast<size_t>(b) * T * cv.stride), 0, T * cv.stride * 2, kBufferRsrcWord3);
+    // raw rows r0-3 .. r0+3 of 8 channels from ch0 (token rows by buffer
+    // load: rows past T read as zeros; rows before token 0 from the ring)
+    struct Raw { u32x4 x[7]; f32x4 rg[3][2]; };
+    auto load_rows = [&](int c0, Raw& o) __attribute__((always_inline)) {
+      const int ch0 = c0 + cc1 * 8;
+#pragma unroll
+      for (int j = 0; j < 7; ++j) {
+        const int t = t0 + r01 - 3 + j;
+        o.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (t * cv.stride + ch0) * 2, 0, 0));
+      }
+      if (t0 + r01 < 3) {   // only the first chunk's first rows reach back before token 0
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const int t = t0 + r01 - 3 + j;
+          const float* rr = cv.ring + (static_cast<size_t>(b) * 3 + (head + 3 + (t < 0 ? t : 0)) % 3) * cv.ch + ch0;
+          o.rg[j][0] = *reinterpret_cast<const f32x4*>(rr);
+          o.rg[j][1] = *reinterpret_cast<const f32x4*>(rr + 4);
+        }
+      }
+    };
+    // conv (4 taps) + SiLU of those rows -> bf16 hi and residual of rows r0 .. r0+3
+    auto conv_tile = [&](int c0, const Raw& in, u32x4 (&hi)[4], u32x4 (&lo)[4]) __attribute__((always_inline)) {
+      const int ch0 = c0 + cc1 * 8;
+      float w[8][4];
+#pragma unroll
+      for (int v4i = 0; v4i < 4; ++v4i) {      // 16 bytes = the taps of two channels
+        const u32x4 r = *reinterpret_cast<const u32x4*>(cv.w + static_cast<size_t>(ch0) * 4 + v4i * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t word = r[e >> 1];
+          w[2 * v4i + (e >> 2)][e & 3] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+        }
+      }
+      float x[7][8];
+#pragma unroll
+      for (int j = 0; j < 7; ++j) {
+        unpack8(in.x[j], x[j]);
+        if (j < 3 && t0 + r01 - 3 + j < 0) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[j][e] = in.rg[j][0][e];
+            x[j][4 + e] = in.rg[j][1][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float acc = x[i][e] * w[e][0];
+          acc += x[i + 1][e] * w[e][1];
+          acc += x[i + 2][e] * w[e][2];
+          acc += x[i + 3][e] * w[e][3];
+          // SiLU from the hardware exp2 and reciprocal (about 1 ulp each,
+          // far below the 2^-16 the hi + lo pair carries)
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-acc * kLog2e));
+          y[e] = (r01 + i < n) ? acc * sg : 0.f;
+        }
+        const u32x4 h = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                         pack_bf16x2(y[6], y[7])};
+        float rsd[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          rsd[e] = y[e] - __uint_as_float((e & 1) ? (h[e >> 1] & 0xffff0000u) : (h[e >> 1] << 16));
+        hi[i] = h;
+        lo[i] = u32x4{pack_bf16x2(rsd[0], rsd[1]), pack_bf16x2(rsd[2], rsd[3]), pack_bf16x2(rsd[4], rsd[5]),
+                      pack_bf16x2(rsd[6], rsd[7])};
+      }
+    };
+    const int qd = Hk * DK;
+    // each tile's rows are in flight while the previous tile is formed
+    Raw ra, rb;
+    load_rows(hk * DK, ra);
+    load_rows(qd + hk * DK, rb);
+    u32x4 hi1[4], lo1[4];
+    conv_tile(hk * DK, ra, hi1, lo1);            // Q; its residual takes the V buffer until P is formed
+    put_rows(sQA, false, hi1);
+    put_rows(sVW, false, lo1);
+    load_rows(2 * qd + hv * DV, ra);
+    conv_tile(qd + hk * DK, rb, hi1, kl1);       // K; its residual first goes to the To buffer
+    put_rows(sK, false, hi1);
+    put_rows(sKl, false, kl1);
+    conv_tile(2 * qd + hv * DV, ra, vh1, vl1);   // V
+  } else {
     const int kq_row = Hk * DK * 2, v_row = Hv * DV * 2;   // source row strides (bytes)
     const u32x4 rk = buffer_rsrc(k + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
     const u32x4 rq = buffer_rsrc(q + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
     const u32x4 rv = buffer_rsrc(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV, (n - 1) * v_row + RB);
-    // split inputs: the query residual takes the V buffer until P is formed
-    // (V is first read by U, after the inverse, and arrives meanwhile)
-    const u32x4 rql = kLo ? buffer_rsrc(q_lo + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK,
-                                        (n - 1) * kq_row + RB)
-                          : rv;
 #pragma unroll
     for (int i = 0; i < kC * NC / kThreads; ++i) {
       const int slot = i * 4 + wave;                       // wave-contiguous KiB
@@ -148,19 +246,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int r = p / NC, cc = p % NC;
       dma16_to_lds(rk, r * kq_row + ((cc ^ swz_rows(r)) << 4), sK + slot * 1024);
       dma16_to_lds(rq, r * kq_row + ((cc ^ swz_rows(r)) << 4), sQA + slot * 1024);
-      if constexpr (kLo) dma16_to_lds(rql, r * kq_row + ((cc ^ swz_rows(r)) << 4), sVW + slot * 1024);
-      else dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
-    }
-    if constexpr (kLo) {
-      // key residual tile into the To buffer, which is free until step 4
-      const u32x4 rl = buffer_rsrc(k_lo + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
-#pragma unroll
-      for (int i = 0; i < kC * NC / kThreads; ++i) {
-        const int slot = i * 4 + wave;
-        const int p = slot * 64 + lane;
-        const int r = p / NC, cc = p % NC;
-        dma16_to_lds(rl, r * kq_row + ((cc ^ swz_rows(r)) << 4), sKl + slot * 1024);
-      }
+      dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
     }
   }
   // gates of this chunk (wave 0, overlapping the DMA): beta, g, prefix sum G
@@ -305,18 +391,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
   }
   __syncthreads();   // Q is no longer read: its space becomes A
-  if constexpr (kLo) {
-    // the query residual is spent: V into its buffer, waited for with V_lo
-    const int v_row = Hv * DV * 2;
-    const u32x4 rv = buffer_rsrc(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV, (n - 1) * v_row + RB);
-#pragma unroll
-    for (int i = 0; i < kC * NC / kThreads; ++i) {
-      const int slot = i * 4 + wave;
-      const int p = slot * 64 + lane;
-      const int r = p / NC, cc = p % NC;
-      dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
-    }
-  }
+  if constexpr (kLo) put_rows(sVW, true, vh1);   // the query residual is spent: V into its buffer
   auto v4 = [&](const float* arr, int i0) __attribute__((always_inline)) { return *reinterpret_cast<const f32x4*>(arr + i0); };
   u32x4* Pout = reinterpret_cast<u32x4*>(rec + R::kP);
 #pragma unroll
@@ -416,22 +491,9 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
     __syncthreads();
   }
-  // Residual tiles by DMA into buffers whose contents are spent: V_lo into
-  // the A space (free once To is formed), later K_lo into the V space.
-  auto dma_tile = [&](const bf16* src_plane, int H, int hidx, bool trswz, unsigned char* dst) __attribute__((always_inline)) {
-    const int row = H * DK * 2;
-    const u32x4 rs = buffer_rsrc(src_plane + (static_cast<size_t>(b) * T + t0) * H * DK + hidx * DK, (n - 1) * row + RB);
-#pragma unroll
-    for (int i = 0; i < kC * NC / kThreads; ++i) {
-      const int slot = i * 4 + wave;
-      const int p = slot * 64 + lane;
-      const int r = p / NC, cc = p % NC;
-      dma16_to_lds(rs, r * row + ((cc ^ (trswz ? swz_tr(r) : swz_rows(r))) << 4), dst + slot * 1024);
-    }
-  };
+  // The V residual into the A space, free once To is formed
   if constexpr (kLo) {
-    dma_tile(v_lo, Hv, hv, true, sQA);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    put_rows(sQA, true, vl1);
     __syncthreads();
   }
 
@@ -501,8 +563,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   }
   if constexpr (kLo) {
     __syncthreads();                        // every wave is done with V
-    dma_tile(k_lo, Hk, hk, false, sVW);     // K residual again (its first copy was overwritten by To)
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    put_rows(sVW, false, kl1);              // K residual again (its first copy was overwritten by To)
     __syncthreads();
   }
   // W^T (operands swapped: A = K^T by transposing reads, B = (To diag(sw))^T):
@@ -826,20 +887,21 @@ size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split) {
   return static_cast<size_t>(B) * Hv * nch * (split ? ChunkRec<128, 128, true>::kBytes : ChunkRec<128, 128, false>::kBytes);
 }
 
-void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const bf16* q_lo, const bf16* k_lo,
-                             const bf16* v_lo,
-                             const bf16* a, const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log,
-                             float* state, bf16* out, unsigned char* records, int B, int T, int Hk, int Hv,
-                             float eps, float scale, hipStream_t st) {
+// conv == nullptr: q, k, v planes (bf16 inputs). Otherwise the layer: q, k,
+// v are formed from conv->qkv by the prep (q, k, v unused).
+void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const ConvIn* conv, const bf16* a,
+                             const bf16* b, int ab_stride, const bf16* dt_bias, const float* A_log, float* state,
+                             bf16* out, unsigned char* records, int B, int T, int Hk, int Hv, float eps, float scale,
+                             hipStream_t st) {
   const int nch = (T + kC - 1) / kC;
-  if (k_lo) {
+  if (conv) {
     hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128, true>), dim3(nch, Hv, B), dim3(kThreads), 0, st, q, k,
-                       v, q_lo, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
+                       v, *conv, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
     hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128, true>), dim3(128 / 16, Hv, B), dim3(2 * kThreads), 0,
                        st, q, records, state, out, T, Hk, Hv, scale);
   } else {
     hipLaunchKernelGGL((deltanet_chunk_prep_kernel<128, 128, false>), dim3(nch, Hv, B), dim3(kThreads), 0, st, q, k,
-                       v, q_lo, k_lo, v_lo, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
+                       v, ConvIn{}, a, b, ab_stride, dt_bias, A_log, records, T, Hk, Hv, eps);
     hipLaunchKernelGGL((deltanet_chunk_scan_kernel<128, 128, false>), dim3(128 / 16, Hv, B), dim3(2 * kThreads), 0,
                        st, q, records, state, out, T, Hk, Hv, scale);
   }
@@ -866,7 +928,7 @@ extern "C" int aila_hip_deltanet_prefill(const void* q, const void* k, const voi
   if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_prefill: workspace %zu < %zu bytes", workspace_bytes, need);
   launch_deltanet_chunked(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                          nullptr, nullptr, nullptr, static_cast<const bf16*>(a), static_cast<const bf16*>(b), Hv,
+                          nullptr, static_cast<const bf16*>(a), static_cast<const bf16*>(b), Hv,
                           static_cast<const bf16*>(dt_bias), A_log, state, static_cast<bf16*>(out),
                           static_cast<unsigned char*>(workspace), B, T, Hk, Hv, eps, scale,
                           static_cast<hipStream_t>(stream));
