@@ -461,6 +461,10 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
                    aligned(z, 16) && z_stride % 8 == 0 && aligned(norm_w, 16) && aligned(state, 16) &&
                    aligned(out, 16),
                "deltanet_layer_prefill: misaligned qkv/conv_w/conv_state/z/norm_w/state/out or odd strides");
+  // a sequence's fused rows are read through one buffer resource (32-bit range)
+  AILA_REQUIRE(static_cast<long>(T) * qkv_stride * 2 < (1L << 31),
+               "deltanet_layer_prefill: T * qkv_stride = %ld elements exceed one 2 GiB range per sequence",
+               static_cast<long>(T) * qkv_stride);
   const size_t need = layer_ws_bytes(B, T, Hv);
   if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_layer_prefill: workspace %zu < %zu bytes", workspace_bytes,
