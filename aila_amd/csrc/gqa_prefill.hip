@@ -719,6 +719,9 @@ extern "C" int aila_hip_gqa_prefill(const void* q, const void* k, const void* v,
   AILA_REQUIRE(S > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq <= 65535,
                "gqa_prefill: bad shape (S=%d Hq=%d Hkv=%d)", S, Hq, Hkv);
   AILA_REQUIRE((k_cache == nullptr) == (v_cache == nullptr), "gqa_prefill: pass both caches or neither");
+  // q and the chunk's K/V are addressed through 32-bit buffer ranges
+  AILA_REQUIRE(static_cast<long>(S) * Hq * D * 2 < (1L << 31),
+               "gqa_prefill: S * Hq * D = %ld elements exceed one 2 GiB range", static_cast<long>(S) * Hq * D);
   if (k_cache) {
     AILA_REQUIRE(cache_pos >= 0 && static_cast<long>(cache_pos) + S <= max_seq,
                  "gqa_prefill: cache rows [%d, %d) exceed max_seq=%d", cache_pos, cache_pos + S, max_seq);
@@ -745,6 +748,8 @@ extern "C" int aila_hip_gqa_prefill_cached_ws(const void* q, const void* k_cache
                "gqa_prefill_cached: bad shape (S=%d start_pos=%d Hq=%d Hkv=%d)", S, start_pos, Hq, Hkv);
   AILA_REQUIRE(static_cast<long>(start_pos) + S <= max_seq,
                "gqa_prefill_cached: start_pos + S = %ld > max_seq=%d", static_cast<long>(start_pos) + S, max_seq);
+  AILA_REQUIRE(static_cast<long>(S) * Hq * D * 2 < (1L << 31) && static_cast<long>(max_seq) * D * 2 < (1L << 31),
+               "gqa_prefill_cached: q or a cache head exceeds one 2 GiB range");
   AILA_REQUIRE(workspace == nullptr || reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                "gqa_prefill_cached: workspace not 16-byte aligned");
   int nz = 1;
