@@ -278,9 +278,10 @@ int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride,
                                    float scale, unsigned int* arrivals,
                                    void* stream);
 
-/* Workspace bytes for aila_hip_deltanet_layer_prefill: the split conv
- * outputs (q; k and v as bf16 hi + bf16 residual planes) and the chunk
- * records with the key residual. 0 for unsupported shapes. */
+/* Workspace bytes for aila_hip_deltanet_layer_prefill: the per-chunk
+ * records (as aila_hip_deltanet_prefill's, plus the key residual; about
+ * 121 KiB per sequence, value head and 64-token chunk). 0 for unsupported
+ * shapes. */
 size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
                                                       int Hv, int dk, int dv);
 
@@ -293,10 +294,13 @@ size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
  * qkv = row, z = row + ch, a = row + ch + Hv*dv, b = a + Hv, every stride the
  * row width). Same math as aila_hip_deltanet_layer_decode applied to the
  * tokens in order, with the ring head advanced per token; the caller
- * advances its head by T afterwards (:1506). The conv outputs stay fp32
- * accurate into the recurrence (hi + lo bf16 planes); the recurrence runs
- * chunked as aila_hip_deltanet_prefill. out [B, T, Hv*dv] bf16. Supported:
- * dk = dv = 128, conv kernel 4, Hv % Hk == 0. */
+ * advances its head by T afterwards (:1506). The chunk prep forms the conv
+ * + SiLU of its rows itself and carries it fp32-accurate (bf16 hi +
+ * residual) into the recurrence, which runs chunked as
+ * aila_hip_deltanet_prefill; the last pass applies the gated RMSNorm and
+ * rewrites the ring. out [B, T, Hv*dv] bf16. Supported: dk = dv = 128,
+ * conv kernel 4, Hv % Hk == 0; qkv 8-byte aligned with qkv_stride a
+ * multiple of 4 and T*qkv_stride*2 < 2^31. */
 int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,
                                     const void* z, int z_stride, const void* a,
                                     const void* b, int ab_stride,
@@ -309,9 +313,10 @@ int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,
                                     int conv_kernel, float eps, float scale,
                                     void* stream);
 
-/* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W, U, P, K^T and
- * decay factors; about 72.8 KiB per (sequence, value head, 64-token chunk)).
- * 0 for unsupported shapes. */
+/* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W and its
+ * residual, U, P, Q, K^T and decay factors, in the scan's operand order;
+ * 105 KiB per (sequence, value head, 64-token chunk)). 0 for unsupported
+ * shapes. */
 size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk,
                                                 int dv);
 
