@@ -119,3 +119,38 @@ def test_graph_replay_paged_decode_and_wide_layer_decode():
         for key in ("o", "lo", "st", "cs", "pk", "pv", "lens", "heads"):
             assert torch.equal(graph_s[key], eager[key]), f"replay {i}: {key} differs"
         assert not graph_s["arr"].any() and not eager["arr"].any()
+
+
+def test_graph_replay_prefill_cached_key_split():
+    """The key-split cached prefill (partial-record pass + merge) captured
+    once and replayed: every replay equals the eager call bit for bit."""
+    import torch
+    import aila_amd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    S, start, Hq, Hkv, D = 96, 1900, 16, 4, 256
+    max_seq = start + S
+    kc = torch.randn((Hkv, max_seq, D), generator=g, **bf)
+    vc = torch.randn((Hkv, max_seq, D), generator=g, **bf)
+    qs = [torch.randn((S, Hq * D), generator=g, **bf) for _ in range(2)]
+    need = aila_amd.gqa_prefill_cached_workspace_size(S, start, Hq, Hkv, D)
+    assert need > 0
+    ws_e = torch.empty(need, dtype=torch.uint8, device="cuda")
+    ws_g = torch.empty(need, dtype=torch.uint8, device="cuda")
+    out_e = torch.empty((S, Hq * D), **bf)
+    out_g = torch.empty((S, Hq * D), **bf)
+    q_in = qs[0].clone()
+    aila_amd.gqa_prefill_cached(q_in, kc, vc, start, Hq, out=out_g, workspace=ws_g)   # warm the path
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        aila_amd.gqa_prefill_cached(q_in, kc, vc, start, Hq, out=out_g, workspace=ws_g)
+    torch.cuda.synchronize()
+    for i in range(4):
+        q_in.copy_(qs[i % 2])
+        aila_amd.gqa_prefill_cached(qs[i % 2], kc, vc, start, Hq, out=out_e, workspace=ws_e)
+        gr.replay()
+        torch.cuda.synchronize()
+        _ = (out_e.float().sum() + 1).item()
+        assert torch.equal(out_g, out_e), f"replay {i}"

@@ -409,3 +409,55 @@ def test_sweep_layer_prefill_then_decode(i, B, Hk, Hv, T, steps, head0, wide):
     assert np.array_equal(cs.cpu().numpy(), want_cs)
     if wide:
         assert not arr.any()
+
+
+def _append_cases():
+    rng = np.random.default_rng(0x5EF2)
+    cases = []
+    for i in range(10):
+        D = int(rng.choice([64, 128, 256]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        Hkv = int(rng.choice([1, 2, 4]))
+        B = int(rng.integers(1, 6))
+        max_seq = int(rng.integers(32, 3000))
+        pos = [int(x) for x in rng.integers(0, max_seq, size=B)]
+        bound = int(rng.integers(max(pos), max_seq))
+        cases.append((i, D, G, Hkv, B, max_seq, bound, pos))
+    return cases
+
+
+@pytest.mark.parametrize("i,D,G,Hkv,B,max_seq,bound,pos", _append_cases())
+def test_sweep_decode_append_device_positions(i, D, G, Hkv, B, max_seq, bound, pos):
+    """Append + split-K decode in one launch at device positions under a host
+    bound (ElementwiseOps.cpp:105-216 cache write, then
+    AttentionOps.cpp:168-320): the row lands bit-exact, every sequence
+    attends rows [0, pos] within tolerance, no other cache row changes."""
+    import torch
+    import aila_amd
+    Hq = Hkv * G
+    seed = 0x5F60 + i
+    print(f"sweep append {i}: D={D} G={G} Hkv={Hkv} B={B} max_seq={max_seq} bound={bound} pos={pos}", flush=True)
+    q = dg.normal_bf16(seed, 0, (B, Hq, D))
+    kn = dg.normal_bf16(seed, 1, (B, Hkv, D))
+    vn = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    kc = dg.normal_bf16(seed, 3, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 4, (B, Hkv, max_seq, D))
+    for b, p in enumerate(pos):
+        kc[b, :, p:] = 0x7FC0
+        vc[b, :, p:] = 0x7FC0
+    dkc, dvc = _t(kc), _t(vc)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out = aila_amd.gqa_decode_append(_t(q), _t(kn), _t(vn), dkc, dvc, bound, workspace=ws,
+                                     positions=_t(np.array(pos, np.int32)))
+    torch.cuda.synchronize()
+    gk, gv = _np(dkc), _np(dvc)
+    for b, p in enumerate(pos):
+        assert np.array_equal(gk[b, :, p], kn[b]) and np.array_equal(gv[b, :, p], vn[b])
+        kc[b, :, p] = kn[b]
+        vc[b, :, p] = vn[b]
+    assert np.array_equal(gk, kc) and np.array_equal(gv, vc)
+    got = dg.bf16_to_f32(_np(out))
+    for b, p in enumerate(pos):
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(q[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv, D,
+                                                               max_seq, p + 1))[0]
+        assert _relerr(got[b], want) <= ATTN_TOL, (b, p)
