@@ -93,6 +93,13 @@ def test_decode_long_context_qwen35_shape():
     _decode_case(3004, 1, 16, 4, 256, 32768 + 8, 32768, split=True, poison=True)
 
 
+def test_decode_128k_context_device_length():
+    # A 128k-row cache (16q/4kv, D=256, 64 MiB per head of K): byte offsets
+    # past 2^31 across the batch/head stride, with the length on the device
+    # (the splits share the actual rows) under a longer capacity bound.
+    _decode_case(3005, 1, 16, 4, 256, 131072 + 16, 131072 + 16, split=True, seq_lens=[131072 - 5])
+
+
 def test_decode_rejects_bad_shapes():
     import torch
     import aila_amd
