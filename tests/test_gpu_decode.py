@@ -94,9 +94,9 @@ def test_decode_long_context_qwen35_shape():
 
 
 def test_decode_128k_context_device_length():
-    # A 128k-row cache (16q/4kv, D=256, 64 MiB per head of K): byte offsets
-    # past 2^31 across the batch/head stride, with the length on the device
-    # (the splits share the actual rows) under a longer capacity bound.
+    # A 128k-row cache (16q/4kv, D=256, 64 MiB of K per head), with the
+    # length on the device (the splits share the actual rows) under a longer
+    # capacity bound.
     _decode_case(3005, 1, 16, 4, 256, 131072 + 16, 131072 + 16, split=True, seq_lens=[131072 - 5])
 
 
