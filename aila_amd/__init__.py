@@ -570,13 +570,18 @@ def decode_prepare_qkv(q_in, k, v, q_norm_w=None, k_norm_w=None, k_cache=None, v
 
 def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_norm_w=None, k_norm_w=None,
                               rotary_dim=None, theta: float = 1e6, eps: float = 1e-6, packed_gate: bool = False,
-                              out=None, gate_out=None, workspace=None, positions=None, stream=None):
+                              out=None, gate_out=None, workspace=None, positions=None, apply_gate: bool = False,
+                              stream=None):
     """QK-norm + RoPE + K/V append + split-K decode in one launch.
     q_in [B,Hq,D] (or [B,Hq,2D] q|gate when packed_gate); k_new/v_new [B,Hkv,D];
     caches [B,Hkv,max_seq,D]. Returns out (and gate_out when packed).
+    apply_gate (packed only): out = attention * sigmoid(gate), the gated
+    attention epilogue, instead of returning the gate.
     Without a workspace the decode runs single-pass (one workgroup per KV
     head), as gqa_decode_append."""
     import torch
+    if apply_gate and not packed_gate:
+        raise ValueError("apply_gate needs packed_gate")
     B, Hkv, max_seq, D = k_cache.shape
     Hq = q_in.shape[1]
     _need(q_in, torch.bfloat16, (B, Hq, 2 * D if packed_gate else D), "q_in")
@@ -590,7 +595,7 @@ def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_
     if out is None:
         out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k_cache.device)
     _need(out, torch.bfloat16, (B, Hq, D), "out")
-    if packed_gate:
+    if packed_gate and not apply_gate:
         if gate_out is None:
             gate_out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=k_cache.device)
         _need(gate_out, torch.bfloat16, (B, Hq, D), "gate_out")
@@ -602,13 +607,14 @@ def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_
     if positions is not None:
         _need(positions, torch.int32, (B,), "positions", align=4)
     rc = lib().aila_hip_gqa_decode_prepare_append(
-        _ptr(q_in), int(bool(packed_gate)), _ptr(gate_out) if packed_gate else None, _ptr(k_new), _ptr(v_new),
+        _ptr(q_in), 2 if apply_gate else int(bool(packed_gate)), _ptr(gate_out) if packed_gate and not apply_gate else None,
+        _ptr(k_new), _ptr(v_new),
         _ptr(q_norm_w), _ptr(k_norm_w), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(workspace),
         ws_bytes, B, Hq, Hkv, D, max_seq,
         D if rotary_dim is None else int(rotary_dim), float(theta), float(eps), int(pos), _ptr(positions),
         _stream(stream))
     _check(rc, "gqa_decode_prepare_append")
-    return (out, gate_out) if packed_gate else out
+    return (out, gate_out) if packed_gate and not apply_gate else out
 
 
 def head_rms_norm(x, weight=None, eps: float = 1e-6, stream=None):

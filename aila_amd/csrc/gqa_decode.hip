@@ -60,6 +60,7 @@ struct PrepArgs {
   const bf16* qn_w;      // [D] or null
   const bf16* kn_w;      // [D] or null
   bf16* gate_out;        // [B, Hq, D] (packed only) or null
+  int apply_gate;        // packed only: out *= sigmoid(gate) instead of copying the gate out
   int rot;               // rotary dims, even, in [2, D]
   float theta, eps;
 };
@@ -465,7 +466,12 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     }
     const int hq = h0 + h;
     if (single) {
-      out[(static_cast<size_t>(b) * Hq + hq) * D + d] = f2bf(Ls > 0.f ? A / Ls : 0.f);
+      float o = Ls > 0.f ? A / Ls : 0.f;
+      if (PREP && pa.apply_gate) {   // gated attention: out * sigmoid(gate) (ElementwiseOps.cpp:519-553)
+        const float g = bf2f(q[(static_cast<size_t>(b) * Hq + hq) * pa.q_stride + D + d]);
+        o *= 1.0f / (1.0f + expf(-g));
+      }
+      out[(static_cast<size_t>(b) * Hq + hq) * D + d] = f2bf(o);
     } else {
       float* rec = part + ((static_cast<size_t>(b) * Hq + hq) * nsplit_max + split) * (kRecHeader + D);
       rec[kRecHeader + d] = A;
@@ -485,7 +491,8 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 template <int D>
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
     const float* __restrict__ part, bf16* __restrict__ out, int Hq, int L,
-    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit, int nsplit_max) {
+    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit, int nsplit_max,
+    const bf16* __restrict__ gate, int gate_stride) {
   constexpr int C4 = D / 4;             // float4 columns
   constexpr int P = 256 / C4;           // split phases
   const int hq = blockIdx.x, b = blockIdx.y;
@@ -562,6 +569,11 @@ __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
 #pragma unroll
     for (int p2 = 1; p2 < P; ++p2) r += s_red[p2][threadIdx.x];
     r *= s_inv;
+    if (gate != nullptr) {   // gated attention: out * sigmoid(gate) (ElementwiseOps.cpp:519-553)
+      const bf16* gr = gate + (static_cast<size_t>(b) * Hq + hq) * gate_stride + 4 * threadIdx.x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] *= 1.0f / (1.0f + expf(-bf2f(gr[j])));
+    }
     const u32x2 w = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
     *reinterpret_cast<u32x2*>(out + (static_cast<size_t>(b) * Hq + hq) * D + 4 * threadIdx.x) = w;
   }
@@ -600,8 +612,10 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
                        a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
   if (a.part) {
+    const bool gated = a.prep.q_stride > 0 && a.prep.apply_gate;
     hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
-                       a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit, a.nsplit_max);
+                       a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit, a.nsplit_max,
+                       gated ? a.q + D : nullptr, a.prep.q_stride);
   }
   return check_launch("gqa_decode");
 }
@@ -832,7 +846,9 @@ extern "C" int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_g
                                                   int pos, const int* positions, void* stream) {
   using namespace aila;
   AILA_REQUIRE(k_new && v_new, "gqa_decode_prepare_append: null k_new/v_new");
-  AILA_REQUIRE(!packed_gate || gate_out, "gqa_decode_prepare_append: packed q|gate needs gate_out");
+  AILA_REQUIRE(packed_gate >= 0 && packed_gate <= 2, "gqa_decode_prepare_append: packed_gate=%d not 0, 1 or 2",
+               packed_gate);
+  AILA_REQUIRE(packed_gate != 1 || gate_out, "gqa_decode_prepare_append: packed q|gate (1) needs gate_out");
   AILA_REQUIRE(pos >= 0 && pos < max_seq, "gqa_decode_prepare_append: pos=%d outside [0, max_seq=%d)", pos,
                max_seq);
   AILA_REQUIRE(theta > 0.f && eps >= 0.f, "gqa_decode_prepare_append: bad theta/eps");
@@ -842,7 +858,8 @@ extern "C" int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_g
   pa.q_stride = packed_gate ? 2 * D : D;
   pa.qn_w = static_cast<const bf16*>(q_norm_w);
   pa.kn_w = static_cast<const bf16*>(k_norm_w);
-  pa.gate_out = packed_gate ? static_cast<bf16*>(gate_out) : nullptr;
+  pa.gate_out = packed_gate == 1 ? static_cast<bf16*>(gate_out) : nullptr;
+  pa.apply_gate = packed_gate == 2;
   pa.rot = rot;
   pa.theta = theta;
   pa.eps = eps;

@@ -501,6 +501,15 @@ def sub_fused_prep_decode(torch, aila_amd, per_graph=8, reps=8):
                                            theta=1e7, packed_gate=True, out=out, gate_out=go, workspace=ws,
                                            positions=pos)
 
+    def fused_gated():
+        aila_amd.gqa_decode_prepare_append(qg, k, v, kc, vc, L, q_norm_w=wq, k_norm_w=wk, rotary_dim=rot,
+                                           theta=1e7, packed_gate=True, apply_gate=True, out=out, workspace=ws,
+                                           positions=pos)
+
+    def fused_then_gate():
+        fused()
+        aila_amd.sigmoid_mul(out, go, out=out)
+
     def two():
         kk.copy_(k)   # decode_prepare_qkv normalises and rotates k in place
         aila_amd.decode_prepare_qkv(qg, kk, v, wq, wk, None, None, positions=pos, rotary_dim=rot, theta=1e7,
@@ -508,7 +517,8 @@ def sub_fused_prep_decode(torch, aila_amd, per_graph=8, reps=8):
         aila_amd.gqa_decode_append(qo, kk, v, kc, vc, L, out=out, workspace=ws, positions=pos)
 
     res = {}
-    for name, fn in (("fused_us", fused), ("two_launch_us", two)):
+    for name, fn in (("fused_us", fused), ("two_launch_us", two), ("fused_gated_us", fused_gated),
+                     ("fused_then_sigmoid_mul_us", fused_then_gate)):
         fn()
         torch.cuda.synchronize()
         gr = torch.cuda.CUDAGraph()
@@ -520,6 +530,8 @@ def sub_fused_prep_decode(torch, aila_amd, per_graph=8, reps=8):
     del kc, vc
     res["config"] = "config-5 GQA layer step B=8 Hq=16 Hkv=4 D=256 L=32768, prep + append + decode"
     res["two_launch_note"] = "includes a 32 KiB device copy of k (the two-launch prep rotates k in place)"
+    res["gated_note"] = ("fused_gated_us applies out *= sigmoid(gate) in the merge (apply_gate); "
+                         "fused_then_sigmoid_mul_us is the same work as two launches")
     return res
 
 

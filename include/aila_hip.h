@@ -140,8 +140,11 @@ int aila_hip_gqa_decode_append(const void* q, const void* k_new,
  * bf16, NeoX RoPE over the first rotary_dim dims at the token's position
  * rounded to bf16, K/V append) followed by ops::attention_decode, as the
  * hybrid backend calls them (Qwen35HybridTextBackend.cpp:2109-2180).
- *   q_in [B, Hq, D] bf16, or [B, Hq, 2D] q|gate per head when packed_gate
- *   (the gate half is copied to gate_out [B, Hq, D]); k_new/v_new
+ *   q_in [B, Hq, D] bf16 (packed_gate 0), or [B, Hq, 2D] q|gate per head:
+ *   packed_gate 1 copies the gate half to gate_out [B, Hq, D]; packed_gate
+ *   2 applies it instead, out = attention * sigmoid(gate) (the gated
+ *   attention epilogue ops::sigmoid_mul, ElementwiseOps.cpp:519-553, in the
+ *   same launch; gate_out unused); k_new/v_new
  *   [B, Hkv, D]; q_norm_w/k_norm_w [D] bf16 or NULL (weight 1). The prepared
  *   k and v_new go to cache row pos (or positions[b]) and sequence b attends
  *   rows [0, row]; q_in and k_new are not modified (the prepared q lives only

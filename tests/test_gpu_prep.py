@@ -205,3 +205,68 @@ def test_fused_prepare_append_decode(B, Hq, Hkv, D, rot, packed, device_pos, spl
                                       positions=_t(pos) if device_pos else None)
     torch.cuda.synchronize()
     _agree(got, _np(out2))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,rot,device_pos,split", [
+    (3, 16, 4, 256, 64, True, True),     # Qwen3.5 attention layer, split-K
+    (3, 16, 4, 256, 64, True, False),    # single pass
+    (2, 8, 1, 128, 32, False, True),
+])
+def test_fused_prepare_append_decode_gated(B, Hq, Hkv, D, rot, device_pos, split):
+    """packed_gate with apply_gate: the gated-attention epilogue
+    (out = attention * sigmoid(gate); Qwen35HybridTextBackend's sigmoid_mul
+    after the attention, ElementwiseOps.cpp:519-553) inside the fused decode
+    launch. Against the oracle's prep + attention + sigmoid_mul, and against
+    the ungated fused launch followed by the sigmoid_mul kernel."""
+    import torch
+    import aila_amd
+    seed, theta, eps, max_seq = 790 + D, 1e7, 1e-6, 2048
+    pos = np.array([5, 700, 2047][:B], np.int32) if device_pos else np.full(B, 1500, np.int32)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
+
+    def run(apply_gate):
+        ws = (torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+              if split else None)
+        kc_d, vc_d = _t(kc), _t(vc)
+        res = aila_amd.gqa_decode_prepare_append(
+            _t(q), _t(k), _t(v), kc_d, vc_d, int(pos.max()), q_norm_w=_t(qw), k_norm_w=_t(kw), rotary_dim=rot,
+            theta=theta, eps=eps, packed_gate=True, apply_gate=apply_gate,
+            positions=_t(pos) if device_pos else None, workspace=ws)
+        torch.cuda.synchronize()
+        return res, kc_d, vc_d
+
+    gated, kc_d, vc_d = run(True)
+    assert isinstance(gated, torch.Tensor) and tuple(gated.shape) == (B, Hq, D)
+    got = _np(gated)
+    qo, gw, ko = oracle.decode_prepare(q, k, v, qw, kw, kc, vc, pos, B, Hq, Hkv, D, max_seq, rot, theta, eps,
+                                       packed=True)
+    for b in range(B):
+        att = oracle.attention_decode_baseline(qo[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv, D, max_seq,
+                                               int(pos[b]) + 1)[0]
+        want = oracle.sigmoid_mul(att, gw[b])
+        assert _relerr(got[b], want) <= TOL, f"sequence {b}"
+    kc_h, vc_h = _np(kc_d), _np(vc_d)
+    for b in range(B):
+        p = int(pos[b])
+        assert np.array_equal(vc_h[b, :, p], v[b])
+        _agree(kc_h[b, :, p], ko[b])
+    (plain, gate), _, _ = run(False)
+    two_step = aila_amd.sigmoid_mul(plain, gate)
+    torch.cuda.synchronize()
+    # one bf16 rounding fewer than the two-launch path: at most one ulp apart
+    ts = _np(two_step)
+    ulps = np.abs(got.astype(np.int32) - ts.astype(np.int32))
+    assert np.all((ulps <= 1) | ((got & 0x7FFF) <= 1) & ((ts & 0x7FFF) <= 1))
+    assert _relerr(got, ts) <= TOL
+
+
+def test_apply_gate_needs_packed():
+    import aila_amd
+    with pytest.raises(ValueError):
+        aila_amd.gqa_decode_prepare_append(None, None, None, None, None, 0, apply_gate=True)
