@@ -115,10 +115,14 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   constexpr int NC = DK / 8;       // 16-byte chunks per row
   __shared__ __attribute__((aligned(1024))) unsigned char sK[kC * RB];    // K, swz_rows
   __shared__ __attribute__((aligned(1024))) unsigned char sQA[kC * RB];   // Q (swz_rows), then A fp32 [64][64]
-  __shared__ __attribute__((aligned(1024))) unsigned char sVW[kC * RB];   // V (swz_tr)
+  // V (swz_tr) for the split inputs; without them V waits in registers
+  // until the A space frees up, which keeps the workgroup at 49.5 KiB of
+  // LDS (three per CU)
+  __shared__ __attribute__((aligned(1024))) unsigned char sVW[kLo ? kC * RB : 16];
   __shared__ __attribute__((aligned(16))) float sT[kC * kC];              // To, fp32 [64][64]
   __shared__ __attribute__((aligned(16))) float sG2[kC], sGn[kC], sBeta[kC], sIk[kC], sIq[kC], sSw[kC];
   float* sA = reinterpret_cast<float*>(sQA);
+  unsigned char* const sV = kLo ? sVW : sQA;   // the V tile for U (transposed swizzle)
   unsigned char* sKl = reinterpret_cast<unsigned char*>(sT);   // K residual (split inputs), steps 1-3
 
   const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
@@ -238,7 +242,9 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const int kq_row = Hk * DK * 2, v_row = Hv * DV * 2;   // source row strides (bytes)
     const u32x4 rk = buffer_rsrc(k + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
     const u32x4 rq = buffer_rsrc(q + (static_cast<size_t>(b) * T + t0) * Hk * DK + hk * DK, (n - 1) * kq_row + RB);
-    const u32x4 rv = buffer_rsrc(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV, (n - 1) * v_row + RB);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(v + (static_cast<size_t>(b) * T + t0) * Hv * DV + hv * DV), 0, (n - 1) * v_row + RB,
+        kBufferRsrcWord3);
 #pragma unroll
     for (int i = 0; i < kC * NC / kThreads; ++i) {
       const int slot = i * 4 + wave;                       // wave-contiguous KiB
@@ -246,8 +252,11 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int r = p / NC, cc = p % NC;
       dma16_to_lds(rk, r * kq_row + ((cc ^ swz_rows(r)) << 4), sK + slot * 1024);
       dma16_to_lds(rq, r * kq_row + ((cc ^ swz_rows(r)) << 4), sQA + slot * 1024);
-      dma16_to_lds(rv, r * v_row + ((cc ^ swz_tr(r)) << 4), sVW + slot * 1024);
     }
+    // V rows r01 .. r01+3, chunk cc1, into registers (rows past T read as zeros)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      vh1[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (r01 + i) * v_row + cc1 * 16, 0, 0));
   }
   // gates of this chunk (wave 0, overlapping the DMA): beta, g, prefix sum G
   if (wave == 0) {
@@ -491,11 +500,11 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
     __syncthreads();
   }
-  // The V residual into the A space, free once To is formed
-  if constexpr (kLo) {
-    put_rows(sQA, true, vl1);
-    __syncthreads();
-  }
+  // The A space is free once To is formed: the V residual (split inputs)
+  // or V itself goes there
+  if constexpr (kLo) put_rows(sQA, true, vl1);
+  else put_rows(sQA, true, vh1);
+  __syncthreads();
 
   // ---- 5. U = bf16(To diag(beta)) V + diag(beta) V, then W likewise with K ----
   // wave w owns token tile w; A operands in slot order over s, B operands by
@@ -539,7 +548,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         if (ks < nks) {
-          const bf16x8_t vb = b_operand(sVW, true, ks, dt);
+          const bf16x8_t vb = b_operand(sV, true, ks, dt);
           acc = mfma16x16x32(au[ks], vb, acc);
           acc = mfma16x16x32(aul[ks], vb, acc);
           if constexpr (kLo) acc = mfma16x16x32(au[ks], b_operand(sQA, true, ks, dt), acc);
@@ -547,7 +556,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       // diagonal term: one transposing read gives V[ti*16 + 4*g4 + j][dt*16 + m16], j = 0..3
       const int vr = ti * 16 + 4 * g4 + (m16 >> 2), vd = dt * 16 + 4 * (m16 & 3);
       const int voff = vr * RB + (((vd >> 3) ^ swz_tr(vr)) << 4) + ((vd & 7) << 1);
-      const u32x2 vv = ds_read_tr4(sVW + voff);
+      const u32x2 vv = ds_read_tr4(sV + voff);
       u32x2 vl = {0u, 0u};
       if constexpr (kLo) vl = ds_read_tr4(sQA + voff);
       const f32x4 bt = v4(sBeta, ti * 16 + g4 * 4);
