@@ -28,8 +28,9 @@
 // thousand tokens. The output-only products (Q S, P D) use single bf16.
 //
 // Kernel 1 (deltanet_chunk_prep_kernel): one workgroup per (chunk, value
-//   head, sequence), fully parallel, two per CU. K, Q, V tiles arrive by
-//   DMA; it writes W, K^T, P, U and the row factors to the workspace, each
+//   head, sequence), fully parallel, three per CU (two with split inputs).
+//   K and Q tiles arrive by DMA, V rows wait in registers for the A space;
+//   it writes W, K^T, P, U and the row factors to the workspace, each
 //   in the register order of the scan's MFMA operands (16-byte loads there).
 // Kernel 2 (deltanet_chunk_scan_kernel): one 8-wave workgroup per (16-column
 //   slab of dv, value head, sequence); walks the chunks in order with its
