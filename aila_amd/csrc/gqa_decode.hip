@@ -707,13 +707,16 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
     a.split_len = 1;
     a.nsplit = 1;
   } else if (workspace) {
-    // One round of resident workgroups; splits are multiples of 128 rows.
+    // One round of resident workgroups; splits are multiples of 64 rows
+    // (one 16-row chunk per wave). Short contexts get one chunk per wave:
+    // config 1 (512 rows, 8 KV heads) takes 6.4 us in 8 splits of 64 rows
+    // against 7.1 us in 4 of 128.
     const int groups = B * Hkv;
     const int resident = resident_for(D, Hq / Hkv);
     int want = (resident + groups - 1) / groups;
     want = std::max(1, std::min(want, a.nsplit_max));
     a.split_len = (cached_len + want - 1) / want;
-    a.split_len = ((a.split_len + 127) / 128) * 128;
+    a.split_len = ((a.split_len + kWaves * kChunk - 1) / (kWaves * kChunk)) * (kWaves * kChunk);
     a.nsplit = (cached_len + a.split_len - 1) / a.split_len;
     if (a.nsplit > 1) a.part = static_cast<float*>(workspace);   // one split: direct output
   } else {
