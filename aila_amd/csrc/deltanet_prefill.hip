@@ -46,6 +46,8 @@
 // workspace stores W (over k), K^T and P (over tokens) in that order.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace aila {
 namespace {
 
@@ -715,30 +717,37 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
 
   if (wave < 4) {
     // ------------------------------------------------------------ state waves
-    auto load = [&](int c, StateOps& o) __attribute__((always_inline)) {
+    // Operands of a chunk in eight parts (0-3: W and W_lo of k-step p;
+    // 4-5: K^T of key tile p-4; 6: its residual; 7: U and the factors). The
+    // parts are issued one per MFMA group of an earlier chunk: the vector
+    // memory path takes ~16 cycles per 1 KiB wave load, and a burst of all
+    // of a chunk's loads stalls the issuing wave - and the phase barrier -
+    // for the whole transfer, where interleaved they hide behind the MFMA
+    // chain.
+    auto load = [&](int c, StateOps& o, int part) __attribute__((always_inline)) {
       const unsigned char* rec = rec_of(c);
-      const u32x4* W = reinterpret_cast<const u32x4*>(rec + R::kW) + w4 * 4 * 64 + lane;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) o.w[ks] = W[ks * 64];
-      const u32x4* WL = reinterpret_cast<const u32x4*>(rec + R::kWLo) + w4 * 4 * 64 + lane;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) o.wl[ks] = WL[ks * 64];
-      const u32x4* Kt = reinterpret_cast<const u32x4*>(rec + R::kKt) + lane;
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      if (part < 4) {
+        o.w[part] = reinterpret_cast<const u32x4*>(rec + R::kW)[(w4 * 4 + part) * 64 + lane];
+        o.wl[part] = reinterpret_cast<const u32x4*>(rec + R::kWLo)[(w4 * 4 + part) * 64 + lane];
+      } else if (part < 6) {
+        const int tt = part - 4;
+        const u32x4* Kt = reinterpret_cast<const u32x4*>(rec + R::kKt) + lane;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = Kt[((w4 * 2 + tt) * 2 + s2) * 64];
-      if constexpr (kLo) {
-        const u32x4* Ktl = reinterpret_cast<const u32x4*>(rec + R::kKtLo) + lane;
+      } else if (part == 6) {
+        if constexpr (kLo) {
+          const u32x4* Ktl = reinterpret_cast<const u32x4*>(rec + R::kKtLo) + lane;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+          for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2) o.kt_lo[tt][s2] = Ktl[((w4 * 2 + tt) * 2 + s2) * 64];
+            for (int s2 = 0; s2 < 2; ++s2) o.kt_lo[tt][s2] = Ktl[((w4 * 2 + tt) * 2 + s2) * 64];
+        }
+      } else {
+        o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + w4) * 64 + lane) * 16);
+        const float* F = reinterpret_cast<const float*>(rec + R::kF);
+        o.fk = *reinterpret_cast<const f32x4*>(F + kC + w4 * 16 + g4 * 4);
+        o.gam = F[2 * kC];
       }
-      o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + w4) * 64 + lane) * 16);
-      const float* F = reinterpret_cast<const float*>(rec + R::kF);
-      o.fk = *reinterpret_cast<const f32x4*>(F + kC + w4 * 16 + g4 * 4);
-      o.gam = F[2 * kC];
     };
     // state slab in C layout: rows 32*w4 + 16*tt + 4*g4 + j, column col
     float* Sg = state + (static_cast<size_t>(b) * Hv + hv) * DK * DV;
@@ -759,11 +768,14 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
                             pack_bf16x2(r[6], r[7])};
     };
     // `active` is uniform; an inactive chunk (past the last one, padding the
-    // three-chunk rotation) only issues its loads and barriers.
-    auto chunk = [&](bool active, const StateOps& o, int cn, StateOps& on) __attribute__((always_inline)) {
+    // three-chunk rotation) computes on repeated operands but keeps its state
+    // (a select, so the chunk body stays one basic block for the schedule).
+    // ROT: this slab's rotation of the load order (see the loop below).
+    auto chunk = [&](bool active, const StateOps& o, int cn, StateOps& on, auto rot_c) __attribute__((always_inline)) {
+      constexpr int ROT = decltype(rot_c)::value;
       // A: D = U - W S (hi*hi + hi*lo + lo*hi), published as bf16 and as
       //    hi/lo bf16 of fk D
-      if (active) {
+      {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < DK / 32; ++ks) {
@@ -771,6 +783,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
         acc = mfma16x16x32(as_bf16x8(o.w[ks]), sh, acc);
         acc = mfma16x16x32(as_bf16x8(o.w[ks]), as_bf16x8(sSl[ks][lane]), acc);
         acc = mfma16x16x32(as_bf16x8(o.wl[ks]), sh, acc);
+        load(cn, on, (ks + 2 * ROT) & 7);
+        __builtin_amdgcn_sched_barrier(0);
       }
       {
         float dval[4], dsc[4], lo[4];
@@ -789,23 +803,29 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
         sDl[s2][half][lane] = u32x2{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3])};
       }
       }
-      load(cn, on);
       phase_barrier();
       // B: S = gamma S + K^T (fk D) for the key rows of this wave
-      if (active) {
+      {
+      bf16x8_t dh[2], dl[2];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        dh[s2] = cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]);
+        dl[s2] = cat8x2(sDl[s2][0][lane], sDl[s2][1][lane]);
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         f32x4 a2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const bf16x8_t aK = as_bf16x8(o.kt[tt][s2]);
-          a2 = mfma16x16x32(aK, cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), a2);
-          a2 = mfma16x16x32(aK, cat8x2(sDl[s2][0][lane], sDl[s2][1][lane]), a2);
-          if constexpr (kLo)
-            a2 = mfma16x16x32(as_bf16x8(o.kt_lo[tt][s2]), cat8x2(sDh[s2][0][lane], sDh[s2][1][lane]), a2);
+          a2 = mfma16x16x32(aK, dh[s2], a2);
+          a2 = mfma16x16x32(aK, dl[s2], a2);
+          if constexpr (kLo) a2 = mfma16x16x32(as_bf16x8(o.kt_lo[tt][s2]), dh[s2], a2);
+          load(cn, on, (4 + 2 * tt + s2 + 2 * ROT) & 7);
+          __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s_reg[tt][j] = o.gam * s_reg[tt][j] + a2[j];
+        for (int j = 0; j < 4; ++j) s_reg[tt][j] = active ? o.gam * s_reg[tt][j] + a2[j] : s_reg[tt][j];
       }
       publish_state();
       }
@@ -814,14 +834,31 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     publish_state();
     // Three operand sets rotate; loads are unconditional (clamped to the
     // last chunk) so that the compiler's wait counts stay exact.
-    StateOps o0, o1, o2;
-    load(0, o0);
-    load(min(1, nch - 1), o1);
-    __syncthreads();
-    for (int c = 0; c < nch; c += 3) {
-      chunk(true, o0, min(c + 2, nch - 1), o2);
-      chunk(c + 1 < nch, o1, min(c + 3, nch - 1), o0);
-      chunk(c + 2 < nch, o2, min(c + 4, nch - 1), o1);
+    // The slabs of a head read the same chunk records at about the same
+    // time; each group of slabs issues the parts in a different order, so
+    // that their requests meet fewer times on one L2 channel.
+    auto run = [&](auto rot_c) __attribute__((always_inline)) {
+      StateOps o0, o1, o2;
+#pragma unroll
+      for (int part = 0; part < 8; ++part) load(0, o0, part);
+#pragma unroll
+      for (int part = 0; part < 8; ++part) load(min(1, nch - 1), o1, part);
+      __syncthreads();
+      for (int c = 0; c < nch; c += 3) {
+        chunk(true, o0, min(c + 2, nch - 1), o2, rot_c);
+        chunk(c + 1 < nch, o1, min(c + 3, nch - 1), o0, rot_c);
+        chunk(c + 2 < nch, o2, min(c + 4, nch - 1), o1, rot_c);
+      }
+    };
+    if constexpr (kLo) {
+      run(std::integral_constant<int, 0>{});   // (four copies of the split-input loop spill)
+    } else {
+      switch (slab & 3) {
+        case 0: run(std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        default: run(std::integral_constant<int, 3>{}); break;
+      }
     }
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
@@ -829,59 +866,74 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       for (int j = 0; j < 4; ++j) Sg[static_cast<size_t>(w4 * 32 + tt * 16 + g4 * 4 + j) * DV + col] = s_reg[tt][j];
   } else {
     // ----------------------------------------------------------- output waves
-    auto load = [&](int c, OutOps& o) __attribute__((always_inline)) {
+    // parts 0-3: Q of k-step p; 4: P and fq (interleaved as in the state waves)
+    auto load = [&](int c, OutOps& o, int part) __attribute__((always_inline)) {
       const unsigned char* rec = rec_of(c);
-      const u32x4* Q = reinterpret_cast<const u32x4*>(rec + R::kQ) + w4 * 4 * 64 + lane;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) o.q[ks] = Q[ks * 64];
-      const u32x4* P = reinterpret_cast<const u32x4*>(rec + R::kP) + w4 * 2 * 64 + lane;
-      o.p[0] = P[0];
-      o.p[1] = P[64];
-      o.fq = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(rec + R::kF) + w4 * 16 + g4 * 4);
+      if (part < 4) {
+        o.q[part] = reinterpret_cast<const u32x4*>(rec + R::kQ)[(w4 * 4 + part) * 64 + lane];
+      } else {
+        const u32x4* P = reinterpret_cast<const u32x4*>(rec + R::kP) + w4 * 2 * 64 + lane;
+        o.p[0] = P[0];
+        o.p[1] = P[64];
+        o.fq = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(rec + R::kF) + w4 * 16 + g4 * 4);
+      }
     };
     // Output rows go out through a buffer resource bounded at the chunk's
     // last token, so the stores need no per-row branch (rows past T drop).
     const int rs2 = Hv * DV * 2;   // bytes per token row
     const int lane_off = ((w4 * 16 + g4 * 4) * Hv + hv) * DV * 2 + col * 2;
-    auto chunk = [&](bool active, int c, const OutOps& o, int cn, OutOps& on) __attribute__((always_inline)) {
+    auto chunk = [&](bool active, int c, const OutOps& o, int cn, OutOps& on, auto rot_c) __attribute__((always_inline)) {
+      constexpr int ROT = decltype(rot_c)::value;
       // A: Q S with the state of this chunk
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      if (active) {
 #pragma unroll
-        for (int ks = 0; ks < DK / 32; ++ks) {
-          const bf16x8_t sh = as_bf16x8(sS[ks][lane]);
-          acc = mfma16x16x32(as_bf16x8(o.q[ks]), sh, acc);
-          // split inputs: S as hi + lo (the residual of Q adds ~15% to the
-          // scan's operand bytes for no measurable gain: P carries it)
-          if constexpr (kLo) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sSl[ks][lane]), acc);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] *= o.fq[j];
+      for (int ks = 0; ks < DK / 32; ++ks) {
+        const bf16x8_t sh = as_bf16x8(sS[ks][lane]);
+        acc = mfma16x16x32(as_bf16x8(o.q[ks]), sh, acc);
+        // split inputs: S as hi + lo (the residual of Q adds ~15% to the
+        // scan's operand bytes for no measurable gain: P carries it)
+        if constexpr (kLo) acc = mfma16x16x32(as_bf16x8(o.q[ks]), as_bf16x8(sSl[ks][lane]), acc);
+        load(cn, on, (ks + ROT) % 5);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      load(cn, on);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] *= o.fq[j];
       phase_barrier();
-      // B: + P D, store
-      if (active) {
+      // B: + P D, store (an inactive chunk's resource holds no bytes)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-          if (s2 <= (w4 >> 1)) acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), acc);
-        const int t0 = c * kC;
-        const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-            out + (static_cast<size_t>(b) * T + t0) * Hv * DV, 0, min(kC, T - t0) * rs2, kBufferRsrcWord3);
+      for (int s2 = 0; s2 < 2; ++s2)
+        if (s2 <= (w4 >> 1)) acc = mfma16x16x32(as_bf16x8(o.p[s2]), cat8x2(sD[s2][0][lane], sD[s2][1][lane]), acc);
+      load(cn, on, (4 + ROT) % 5);
+      const int t0 = min(c, nch - 1) * kC;
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          out + (static_cast<size_t>(b) * T + t0) * Hv * DV, 0, active ? min(kC, T - t0) * rs2 : 0, kBufferRsrcWord3);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * acc[j]), orsrc, lane_off + j * rs2, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(scale * acc[j]), orsrc, lane_off + j * rs2, 0, 0);
       phase_barrier();
     };
-    OutOps o0, o1, o2;
-    load(0, o0);
-    load(min(1, nch - 1), o1);
-    __syncthreads();
-    for (int c = 0; c < nch; c += 3) {
-      chunk(true, c, o0, min(c + 2, nch - 1), o2);
-      chunk(c + 1 < nch, c + 1, o1, min(c + 3, nch - 1), o0);
-      chunk(c + 2 < nch, c + 2, o2, min(c + 4, nch - 1), o1);
+    auto run = [&](auto rot_c) __attribute__((always_inline)) {   // load orders as in the state waves
+      OutOps o0, o1, o2;
+#pragma unroll
+      for (int part = 0; part < 5; ++part) load(0, o0, part);
+#pragma unroll
+      for (int part = 0; part < 5; ++part) load(min(1, nch - 1), o1, part);
+      __syncthreads();
+      for (int c = 0; c < nch; c += 3) {
+        chunk(true, c, o0, min(c + 2, nch - 1), o2, rot_c);
+        chunk(c + 1 < nch, c + 1, o1, min(c + 3, nch - 1), o0, rot_c);
+        chunk(c + 2 < nch, c + 2, o2, min(c + 4, nch - 1), o1, rot_c);
+      }
+    };
+    if constexpr (kLo) {
+      run(std::integral_constant<int, 0>{});   // (four copies of the split-input loop spill)
+    } else {
+      switch (slab & 3) {
+        case 0: run(std::integral_constant<int, 0>{}); break;
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        default: run(std::integral_constant<int, 3>{}); break;
+      }
     }
   }
 }
