@@ -211,6 +211,8 @@ def test_fused_prepare_append_decode(B, Hq, Hkv, D, rot, packed, device_pos, spl
     (3, 16, 4, 256, 64, True, True),     # Qwen3.5 attention layer, split-K
     (3, 16, 4, 256, 64, True, False),    # single pass
     (2, 8, 1, 128, 32, False, True),
+    (1, 8, 8, 64, 64, True, True),       # G = 1, D = 64, first row of the cache (pos 5)
+    (3, 16, 2, 128, 128, True, False),   # G = 8 single pass, full rotary
 ])
 def test_fused_prepare_append_decode_gated(B, Hq, Hkv, D, rot, device_pos, split):
     """packed_gate with apply_gate: the gated-attention epilogue
