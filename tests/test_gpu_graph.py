@@ -154,3 +154,55 @@ def test_graph_replay_prefill_cached_key_split():
         torch.cuda.synchronize()
         _ = (out_e.float().sum() + 1).item()
         assert torch.equal(out_g, out_e), f"replay {i}"
+
+
+def test_graph_replay_chunked_prefills():
+    """The chunked DeltaNet prefill and the whole-layer prefill (whose scan
+    holds four copies of its loop and spills registers) captured in one
+    graph with the state reset inside it: every replay, with eager work in
+    between, equals the eager call bit for bit."""
+    import torch
+    import aila_amd
+    g = torch.Generator(device="cuda")
+    g.manual_seed(321)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    B, T, Hk, Hv, d = 1, 200, 2, 4, 128
+    ch = 2 * Hk * d + Hv * d
+    q = torch.randn((B, T, Hk, d), generator=g, **bf)
+    k = torch.randn((B, T, Hk, d), generator=g, **bf)
+    v = torch.randn((B, T, Hv, d), generator=g, **bf)
+    a = torch.randn((B, T, Hv), generator=g, **bf)
+    b = torch.randn((B, T, Hv), generator=g, **bf)
+    qkv = torch.randn((B, T, ch), generator=g, **bf)
+    z = torch.randn((B, T, Hv * d), generator=g, **bf)
+    conv_w = torch.randn((ch, 4), generator=g, **bf) * 0.5
+    norm_w = 1.0 + 0.1 * torch.randn(d, generator=g, device="cuda")
+    s0 = torch.randn((B, Hv, d, d), generator=g, device="cuda") * 0.02
+    cs0 = torch.randn((B, 3, ch), generator=g, device="cuda")
+    ws = torch.empty(aila_amd.deltanet_prefill_workspace_size(B, T, Hv, d, d), dtype=torch.uint8, device="cuda")
+    wsl = torch.empty(aila_amd.deltanet_layer_prefill_workspace_size(B, T, Hk, Hv), dtype=torch.uint8, device="cuda")
+
+    def make():
+        return dict(st=s0.clone(), stl=s0.clone(), cs=cs0.clone(), o=torch.empty((B, T, Hv, d), **bf),
+                    ol=torch.empty((B, T, Hv * d), **bf))
+
+    def run(S):
+        S["st"].copy_(s0)
+        S["stl"].copy_(s0)
+        S["cs"].copy_(cs0)
+        aila_amd.deltanet_prefill(q, k, v, a, b, S["st"], out=S["o"], workspace=ws)
+        aila_amd.deltanet_layer_prefill(qkv, z, a, b, conv_w, S["cs"], 1, norm_w, S["stl"], Hk, out=S["ol"],
+                                        workspace=wsl)
+
+    eager, graph_s = make(), make()
+    run(eager)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        run(graph_s)
+    for i in range(3):
+        gr.replay()
+        torch.cuda.synchronize()
+        _ = (eager["o"].float().sum() + 1).item()   # unrelated eager work between replays
+        for key in ("st", "stl", "cs", "o", "ol"):
+            assert torch.equal(graph_s[key], eager[key]), f"replay {i}: {key} differs"
