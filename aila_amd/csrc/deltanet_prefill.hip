@@ -27,6 +27,10 @@
 // bf16 roundings there would grow the state error past 1e-3 within a few
 // thousand tokens. The output-only products (Q S, P D) use single bf16.
 //
+// The prep writes the records with nontemporal stores: each is read once,
+// by the scan, after the whole prep has run (layer prefill at config 4:
+// 258 -> 242 us, most of it in the scan's reads of them).
+//
 // Kernel 1 (deltanet_chunk_prep_kernel): one workgroup per (chunk, value
 //   head, sequence), fully parallel, three per CU (two with split inputs).
 //   K and Q tiles arrive by DMA, V rows wait in registers for the A space;
@@ -351,7 +355,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int a1 = r * RB + (((k1 >> 3) ^ swz_rows(r)) << 4) + ((k1 & 7) << 1);
       const u32x2 lo = *reinterpret_cast<const u32x2*>(sQA + a0);
       const u32x2 hi = *reinterpret_cast<const u32x2*>(sQA + a1);
-      Qout[o] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      __builtin_nontemporal_store(u32x4{lo[0], lo[1], hi[0], hi[1]}, &Qout[o]);
     }
   }
 
@@ -434,8 +438,8 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
         for (int j = 0; j < 4; ++j)
           pv[4 * h + j] = (s0 + j <= t) ? iqt * iks[j] * fast_exp2(g2t - g2s[j]) * acc3[i][h][j] : 0.f;
       }
-      Pout[(ti * 2 + s2) * 64 + lane] = u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
-                                              pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7])};
+      __builtin_nontemporal_store(u32x4{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
+                                              pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7])}, &Pout[(ti * 2 + s2) * 64 + lane]);
     }
   }
   __syncthreads();
@@ -570,7 +574,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
         if constexpr (kLo) vf += __uint_as_float((j & 1) ? (vl[j >> 1] & 0xffff0000u) : (vl[j >> 1] << 16));
         u[j] = acc[j] + bt[j] * vf;
       }
-      *reinterpret_cast<f32x4*>(&Uout[((dt * 4 + ti) * 64 + lane) * 4]) = u;   // C-layout order
+      __builtin_nontemporal_store(u, reinterpret_cast<f32x4*>(&Uout[((dt * 4 + ti) * 64 + lane) * 4]));
     }
   }
   if constexpr (kLo) {
@@ -622,9 +626,9 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       float wr[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) wr[e] = wv[e] - __uint_as_float((e & 1) ? (wh[e >> 1] & 0xffff0000u) : (wh[e >> 1] << 16));
-      Wout[(ti * 4 + kso) * 64 + lane] = wh;
-      WLout[(ti * 4 + kso) * 64 + lane] = u32x4{pack_bf16x2(wr[0], wr[1]), pack_bf16x2(wr[2], wr[3]),
-                                                pack_bf16x2(wr[4], wr[5]), pack_bf16x2(wr[6], wr[7])};
+      __builtin_nontemporal_store(wh, &Wout[(ti * 4 + kso) * 64 + lane]);
+      __builtin_nontemporal_store(u32x4{pack_bf16x2(wr[0], wr[1]), pack_bf16x2(wr[2], wr[3]),
+                                                pack_bf16x2(wr[4], wr[5]), pack_bf16x2(wr[6], wr[7])}, &WLout[(ti * 4 + kso) * 64 + lane]);
     }
   }
   // ---- 6. K^T in slot order over tokens, straight from transposing reads --------
@@ -636,10 +640,11 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       const int job = wave * (2 * (DK / 16) / 4) + i;
       const int ks = job & 1, dt = job >> 1;
       const bf16x8_t op = b_operand(sK, false, ks, dt);   // K[tokens in slot order][dt*16 + m16]
-      *reinterpret_cast<u32x4*>(&Ktout[((dt * 2 + ks) * 64 + lane) * 8]) = __builtin_bit_cast(u32x4, op);
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, op), reinterpret_cast<u32x4*>(&Ktout[((dt * 2 + ks) * 64 + lane) * 8]));
       if constexpr (kLo) {
         const bf16x8_t ol = b_operand(sVW, false, ks, dt);
-        *reinterpret_cast<u32x4*>(rec + R::kKtLo + ((dt * 2 + ks) * 64 + lane) * 16) = __builtin_bit_cast(u32x4, ol);
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, ol),
+                                    reinterpret_cast<u32x4*>(rec + R::kKtLo + ((dt * 2 + ks) * 64 + lane) * 16));
       }
     }
   }
