@@ -258,7 +258,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
         for (int dt = 0; dt < C::DT; ++dt) {
           const f32x4 o = o_acc[dt][qt] * inv;
           const u32x2 w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-          *reinterpret_cast<u32x2*>(orow + dt * 16) = w;
+          // outputs and cache rows are written once and not read back by
+          // this kernel: nontemporal (config 2: 50.5 -> 48.5 us)
+          __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(orow + dt * 16));
         }
       }
     }
@@ -428,8 +430,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
           const int row = r0 + gi + (p / C::NC) * G, c = p % C::NC;
           const size_t src = static_cast<size_t>(row) * kv_row_stride + c * 8;
           const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + row) * D + c * 8;
-          *reinterpret_cast<u32x4*>(k_cache + dst) = ld16(Kh + src);
-          *reinterpret_cast<u32x4*>(v_cache + dst) = ld16(Vh + src);
+          __builtin_nontemporal_store(ld16(Kh + src), reinterpret_cast<u32x4*>(k_cache + dst));
+          __builtin_nontemporal_store(ld16(Vh + src), reinterpret_cast<u32x4*>(v_cache + dst));
         }
       }
     }
