@@ -664,7 +664,6 @@ struct StateOps {
   u32x4 w[4];        // W rows of token tile w4, k-steps 0..3 (slot order)
   u32x4 wl[4];       // residual of W
   u32x4 kt[2][2];    // K^T rows [key tile][token k-step]
-  u32x4 kt_lo[2][2]; // residual of K^T (split inputs only; unused and dropped otherwise)
   f32x4 u;           // U (C layout)
   f32x4 fk;          // fk of the 4 rows this lane holds
   float gam;
@@ -723,12 +722,11 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
   if (wave < 4) {
     // ------------------------------------------------------------ state waves
     // Operands of a chunk in eight parts (0-3: W and W_lo of k-step p;
-    // 4-5: K^T of key tile p-4; 6: its residual; 7: U and the factors). The
-    // parts are issued one per MFMA group of an earlier chunk: the vector
-    // memory path takes ~16 cycles per 1 KiB wave load, and a burst of all
-    // of a chunk's loads stalls the issuing wave - and the phase barrier -
-    // for the whole transfer, where interleaved they hide behind the MFMA
-    // chain.
+    // 4-5: K^T of key tile p-4; 7: U and the factors; 6 is empty - the K^T
+    // residual of split inputs is loaded by its own chunk, half a chunk
+    // ahead of its use, which keeps that variant within the register file).
+    // The parts are issued one per MFMA group of an earlier chunk, in an
+    // order that differs between slabs (below).
     auto load = [&](int c, StateOps& o, int part) __attribute__((always_inline)) {
       const unsigned char* rec = rec_of(c);
       if (part < 4) {
@@ -740,13 +738,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = Kt[((w4 * 2 + tt) * 2 + s2) * 64];
       } else if (part == 6) {
-        if constexpr (kLo) {
-          const u32x4* Ktl = reinterpret_cast<const u32x4*>(rec + R::kKtLo) + lane;
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) o.kt_lo[tt][s2] = Ktl[((w4 * 2 + tt) * 2 + s2) * 64];
-        }
+        // (the K^T residual of split inputs is loaded by the chunk itself)
       } else {
         o.u = *reinterpret_cast<const f32x4*>(rec + R::kU + ((slab * 4 + w4) * 64 + lane) * 16);
         const float* F = reinterpret_cast<const float*>(rec + R::kF);
@@ -776,7 +768,17 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     // three-chunk rotation) computes on repeated operands but keeps its state
     // (a select, so the chunk body stays one basic block for the schedule).
     // ROT: this slab's rotation of the load order (see the loop below).
-    auto chunk = [&](bool active, const StateOps& o, int cn, StateOps& on, auto rot_c) __attribute__((always_inline)) {
+    auto chunk = [&](bool active, const StateOps& o, int cc, int cn, StateOps& on, auto rot_c) __attribute__((always_inline)) {
+      // split inputs: the K^T residual of this chunk, loaded now (half a
+      // chunk ahead of its use) instead of in the rotating sets
+      u32x4 ktl[2][2];
+      if constexpr (kLo) {
+        const u32x4* Ktl = reinterpret_cast<const u32x4*>(rec_of(min(cc, nch - 1)) + R::kKtLo) + lane;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) ktl[tt][s2] = Ktl[((w4 * 2 + tt) * 2 + s2) * 64];
+      }
       constexpr int ROT = decltype(rot_c)::value;
       // A: D = U - W S (hi*hi + hi*lo + lo*hi), published as bf16 and as
       //    hi/lo bf16 of fk D
@@ -825,7 +827,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
           const bf16x8_t aK = as_bf16x8(o.kt[tt][s2]);
           a2 = mfma16x16x32(aK, dh[s2], a2);
           a2 = mfma16x16x32(aK, dl[s2], a2);
-          if constexpr (kLo) a2 = mfma16x16x32(as_bf16x8(o.kt_lo[tt][s2]), dh[s2], a2);
+          if constexpr (kLo) a2 = mfma16x16x32(as_bf16x8(ktl[tt][s2]), dh[s2], a2);
           load(cn, on, (4 + 2 * tt + s2 + 2 * ROT) & 7);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -842,8 +844,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     // The slabs of a head read the same chunk records at about the same
     // time; each group of slabs issues the parts in a different order, so
     // that their requests meet fewer times on one L2 channel (config 4:
-    // 171 -> 160 us; the layer's split-input scan spills ~54 registers with
-    // the four copies of the loop and still gains, 271 -> 258 us).
+    // 171 -> 160 us; layer prefill 271 -> 258 us).
     auto run = [&](auto rot_c) __attribute__((always_inline)) {
       StateOps o0, o1, o2;
 #pragma unroll
@@ -852,9 +853,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       for (int part = 0; part < 8; ++part) load(min(1, nch - 1), o1, part);
       __syncthreads();
       for (int c = 0; c < nch; c += 3) {
-        chunk(true, o0, min(c + 2, nch - 1), o2, rot_c);
-        chunk(c + 1 < nch, o1, min(c + 3, nch - 1), o0, rot_c);
-        chunk(c + 2 < nch, o2, min(c + 4, nch - 1), o1, rot_c);
+        chunk(true, o0, c, min(c + 2, nch - 1), o2, rot_c);
+        chunk(c + 1 < nch, o1, c + 1, min(c + 3, nch - 1), o0, rot_c);
+        chunk(c + 2 < nch, o2, c + 2, min(c + 4, nch - 1), o1, rot_c);
       }
     };
     switch (slab & 3) {
