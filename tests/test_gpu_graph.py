@@ -157,10 +157,10 @@ def test_graph_replay_prefill_cached_key_split():
 
 
 def test_graph_replay_chunked_prefills():
-    """The chunked DeltaNet prefill and the whole-layer prefill (whose scan
-    holds four copies of its loop and spills registers) captured in one
-    graph with the state reset inside it: every replay, with eager work in
-    between, equals the eager call bit for bit."""
+    """The chunked DeltaNet prefill and the whole-layer prefill (four copies
+    of the scan loop, one per slab load order) captured in one graph with
+    the state reset inside it: every replay, with eager work in between,
+    equals the eager call bit for bit."""
     import torch
     import aila_amd
     g = torch.Generator(device="cuda")
