@@ -33,7 +33,7 @@ _SIGS = {
     "aila_hip_gqa_decode_noalloc": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_decode_append": ([_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_decode_prepare_append": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I,
-                                            _I, _F, _F, _I, _P, _P], _I),
+                                            _I, _F, _F, _I, _P, _P, _P], _I),
     "aila_hip_kv_append": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "aila_hip_gqa_prefill": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "aila_hip_gqa_prefill_cached": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -49,9 +49,9 @@ _SIGS = {
     "aila_hip_deltanet_layer_decode": ([_P, _I, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P,
                                         _I, _I, _I, _I, _I, _I, _F, _F, _P, _P], _I),
     "aila_hip_decode_prepare_qkv": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
-                                     _I, _I, _I, _I, _I, _I, _F, _F, _I, _P, _P], _I),
+                                     _I, _I, _I, _I, _I, _I, _F, _F, _I, _P, _P, _P], _I),
     "aila_hip_head_rms_norm": ([_P, _P, _I, _I, _I, _F, _P], _I),
-    "aila_hip_apply_rope": ([_P, _P, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "aila_hip_apply_rope": ([_P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P], _I),
     "aila_hip_sigmoid_mul": ([_P, _P, _P, ctypes.c_long, _P], _I),
     "aila_hip_deltanet_prefill": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ,
                                    _I, _I, _I, _I, _I, _I, _F, _F, _P], _I),
@@ -113,6 +113,56 @@ def _need(t, dtype, shape, name, align=16):
     if t.data_ptr() % align:
         raise ValueError(f"{name} must be {align}-byte aligned")
     del torch
+
+
+class RopePos(ctypes.Structure):
+    """``aila_hip_rope_pos``: rotary positions that differ from the cache row
+    (text shift past the prompt and interleaved mRoPE streams, the reference's
+    apply_rope_partial arguments). Build it with :func:`rope_pos`."""
+    _fields_ = [("interleaved", _I), ("pos_t", _P), ("pos_h", _P), ("pos_w", _P),
+                ("pos_stride", _I), ("prompt_pos_len", _I), ("text_pos_delta", _I),
+                ("prompt_pos_lens", _P), ("text_pos_deltas", _P),
+                ("mrope_section_t", _I), ("mrope_section_h", _I), ("mrope_section_w", _I)]
+
+
+def rope_pos(prompt_pos_len: int = 0, text_pos_delta: int = 0, pos_t=None, pos_h=None, pos_w=None,
+             interleaved: bool = True, sections=(0, 0, 0), prompt_pos_lens=None, text_pos_deltas=None):
+    """Rotary position record. pos_t/pos_h/pos_w: device int32 [P] (one prompt,
+    shared by every sequence) or [B, P] (per sequence); prompt_pos_lens /
+    text_pos_deltas: optional device int32 [B] overriding the scalars."""
+    import torch
+    rp = RopePos()
+    rp.interleaved = int(bool(interleaved))
+    rp.prompt_pos_len = int(prompt_pos_len)
+    rp.text_pos_delta = int(text_pos_delta)
+    rp.mrope_section_t, rp.mrope_section_h, rp.mrope_section_w = (int(x) for x in sections)
+    keep = []
+    streams = (pos_t, pos_h, pos_w)
+    if any(t is not None for t in streams):
+        if any(t is None for t in streams):
+            raise ValueError("pos_t, pos_h and pos_w go together")
+        shape = tuple(pos_t.shape)
+        if len(shape) not in (1, 2):
+            raise ValueError("position streams must be [P] or [B, P]")
+        for t, name in zip(streams, ("pos_t", "pos_h", "pos_w")):
+            _need(t, torch.int32, shape, name, align=4)
+            keep.append(t)
+        rp.pos_t, rp.pos_h, rp.pos_w = (t.data_ptr() for t in streams)
+        rp.pos_stride = shape[1] if len(shape) == 2 else 0
+    for t, name in ((prompt_pos_lens, "prompt_pos_lens"), (text_pos_deltas, "text_pos_deltas")):
+        if t is not None:
+            _need(t, torch.int32, tuple(t.shape), name, align=4)
+            keep.append(t)
+    if prompt_pos_lens is not None:
+        rp.prompt_pos_lens = prompt_pos_lens.data_ptr()
+    if text_pos_deltas is not None:
+        rp.text_pos_deltas = text_pos_deltas.data_ptr()
+    rp._keep = keep   # the device arrays must outlive the launches that read them
+    return rp
+
+
+def _rope_arg(rope):
+    return None if rope is None else ctypes.byref(rope)
 
 
 # ----------------------------------------------------------------- GQA ----
@@ -530,12 +580,13 @@ def deltanet_prefill(q, k, v, a, b, state, out=None, workspace=None, dt_bias=Non
 def decode_prepare_qkv(q_in, k, v, q_norm_w=None, k_norm_w=None, k_cache=None, v_cache=None,
                        pos: int = 0, positions=None, rotary_dim=None, theta: float = 1e6,
                        eps: float = 1e-6, packed_gate: bool = False, q_out=None, gate_out=None,
-                       stream=None):
+                       rope=None, stream=None):
     """Per-head RMSNorm + RoPE of one token per sequence, and the K/V append.
 
     q_in [B,Hq,D] (or [B,Hq,2D] q|gate when ``packed_gate``); k [B,Hkv,D] is
     updated in place; v [B,Hkv,D]; caches [B,Hkv,max_seq,D] or None. Returns
-    q_out (and gate_out when packed)."""
+    q_out (and gate_out when packed). rope: a :func:`rope_pos` record (text
+    shift / mRoPE positions); None rotates at the cache row."""
     import torch
     B, Hkv, D = k.shape
     Hq = q_in.shape[1]
@@ -563,7 +614,7 @@ def decode_prepare_qkv(q_in, k, v, q_norm_w=None, k_norm_w=None, k_cache=None, v
         _ptr(q_in), int(bool(packed_gate)), _ptr(q_out), _ptr(gate_out) if packed_gate else None,
         _ptr(k), _ptr(v), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(k_cache), _ptr(v_cache), B, Hq, Hkv, D,
         max_seq, D if rotary_dim is None else int(rotary_dim), float(theta), float(eps), int(pos),
-        _ptr(positions), _stream(stream))
+        _ptr(positions), _rope_arg(rope), _stream(stream))
     _check(rc, "decode_prepare_qkv")
     return (q_out, gate_out) if packed_gate else q_out
 
@@ -571,7 +622,7 @@ def decode_prepare_qkv(q_in, k, v, q_norm_w=None, k_norm_w=None, k_cache=None, v
 def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_norm_w=None, k_norm_w=None,
                               rotary_dim=None, theta: float = 1e6, eps: float = 1e-6, packed_gate: bool = False,
                               out=None, gate_out=None, workspace=None, positions=None, apply_gate: bool = False,
-                              stream=None):
+                              rope=None, stream=None):
     """QK-norm + RoPE + K/V append + split-K decode in one launch.
     q_in [B,Hq,D] (or [B,Hq,2D] q|gate when packed_gate); k_new/v_new [B,Hkv,D];
     caches [B,Hkv,max_seq,D]. Returns out (and gate_out when packed).
@@ -612,7 +663,7 @@ def gqa_decode_prepare_append(q_in, k_new, v_new, k_cache, v_cache, pos: int, q_
         _ptr(q_norm_w), _ptr(k_norm_w), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(workspace),
         ws_bytes, B, Hq, Hkv, D, max_seq,
         D if rotary_dim is None else int(rotary_dim), float(theta), float(eps), int(pos), _ptr(positions),
-        _stream(stream))
+        _rope_arg(rope), _stream(stream))
     _check(rc, "gqa_decode_prepare_append")
     return (out, gate_out) if packed_gate and not apply_gate else out
 
@@ -629,8 +680,9 @@ def head_rms_norm(x, weight=None, eps: float = 1e-6, stream=None):
     return x
 
 
-def apply_rope(q, k, start_pos: int = 0, rotary_dim=None, theta: float = 1e6, stream=None):
-    """In-place RoPE of q [S,Hq,D] and k [S,Hkv,D] bf16 at positions start_pos + s."""
+def apply_rope(q, k, start_pos: int = 0, rotary_dim=None, theta: float = 1e6, rope=None, stream=None):
+    """In-place RoPE of q [S,Hq,D] and k [S,Hkv,D] bf16 for the tokens of cache
+    rows start_pos + s (at those rows, or at the positions of ``rope``)."""
     import torch
     S, Hq, D = q.shape
     Hkv = k.shape[1]
@@ -638,7 +690,7 @@ def apply_rope(q, k, start_pos: int = 0, rotary_dim=None, theta: float = 1e6, st
     _need(k, torch.bfloat16, (S, Hkv, D), "k")
     _check(lib().aila_hip_apply_rope(_ptr(q), _ptr(k), S, int(start_pos), Hq, Hkv, D,
                                      D if rotary_dim is None else int(rotary_dim), float(theta),
-                                     _stream(stream)), "apply_rope")
+                                     _rope_arg(rope), _stream(stream)), "apply_rope")
     return q, k
 
 

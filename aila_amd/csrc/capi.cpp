@@ -25,8 +25,21 @@ int check_launch(const char* what) {
   return AILA_HIP_OK;
 }
 
+int load_rope_pos(const aila_hip_rope_pos* rp, aila_hip_rope_pos* out, const char* what) {
+  *out = aila_hip_rope_pos{};
+  if (rp == nullptr) return AILA_HIP_OK;
+  if (rp->prompt_pos_len < 0 && rp->prompt_pos_lens == nullptr)
+    return set_error(AILA_HIP_EINVAL, "%s: prompt_pos_len=%d < 0", what, rp->prompt_pos_len);
+  const bool mrope = rp->interleaved && rp->pos_t && rp->pos_h && rp->pos_w;
+  if (mrope && (rp->pos_stride < 0 || rp->mrope_section_h < 0 || rp->mrope_section_w < 0))
+    return set_error(AILA_HIP_EINVAL, "%s: bad mRoPE streams (pos_stride=%d sections h=%d w=%d)", what,
+                     rp->pos_stride, rp->mrope_section_h, rp->mrope_section_w);
+  *out = *rp;
+  return AILA_HIP_OK;
+}
+
 }  // namespace aila
 
 extern "C" const char* aila_hip_last_error(void) { return aila::g_last_error; }
 
-extern "C" int aila_hip_version(void) { return (1 << 16) | 0; }
+extern "C" int aila_hip_version(void) { return (1 << 16) | 1; }

@@ -214,12 +214,57 @@ struct ConvIn {
   int ch;              // channels of a row's [q | k | v] part
 };
 
+// ---- rotary positions (text shift and interleaved mRoPE) -----------------
+// The device copy of aila_hip_rope_pos, passed by value as a kernel argument
+// (a zero struct = rotate at the cache row). Reference:
+// ops::apply_rope_partial and the decode_prepare_*_partial rotary_position
+// lambda, src/ops/ElementwiseOps.cpp:33-103, 555-863.
+typedef aila_hip_rope_pos RopePos;
+
+// Positions of the token in cache row `row` of sequence b: the scalar
+// position (row, shifted by the text delta past the prompt) and the three
+// mRoPE stream values (all equal to the scalar unless the row lies inside a
+// prompt that carries position streams).
+struct RowPos {
+  int t, h, w;
+  int sec_h, sec_w;
+};
+
+__device__ __forceinline__ RowPos rope_row_pos(const RopePos& rp, int b, int row) {
+  const int plen = rp.prompt_pos_lens ? rp.prompt_pos_lens[b] : rp.prompt_pos_len;
+  const int delta = rp.text_pos_deltas ? rp.text_pos_deltas[b] : rp.text_pos_delta;
+  const int scalar = row >= plen ? row + delta : row;
+  RowPos p{scalar, scalar, scalar, 0, 0};
+  if (rp.interleaved && rp.pos_t && rp.pos_h && rp.pos_w) {
+    p.sec_h = rp.mrope_section_h;
+    p.sec_w = rp.mrope_section_w;
+    if (row < plen) {
+      const size_t i = static_cast<size_t>(b) * rp.pos_stride + row;
+      p.t = rp.pos_t[i];
+      p.h = rp.pos_h[i];
+      p.w = rp.pos_w[i];
+    }
+  }
+  return p;
+}
+
+// Position rotating frequency index j (0 <= j < rot/2).
+__device__ __forceinline__ float rope_freq_pos(const RowPos& p, int j) {
+  const int m = j % 3, q = j / 3;
+  if (m == 1 && q < p.sec_h) return static_cast<float>(p.h);
+  if (m == 2 && q < p.sec_w) return static_cast<float>(p.w);
+  return static_cast<float>(p.t);
+}
+
 }  // namespace aila
 
 // ---- host-side error plumbing (defined in capi.hip) ---------------------
 namespace aila {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Copies *rp (NULL: zero struct) after checking its fields; returns 0 or an
+// AILA_HIP_EINVAL set_error code.
+int load_rope_pos(const aila_hip_rope_pos* rp, RopePos* out, const char* what);
 }  // namespace aila
 
 #define AILA_REQUIRE(cond, ...)                                  \

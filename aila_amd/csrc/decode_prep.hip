@@ -48,9 +48,11 @@ __device__ __forceinline__ void norm_head_to_lds(const bf16* __restrict__ x, con
   }
 }
 
-// RoPE from the rounded normalised head in LDS to `y` (bf16).
+// RoPE from the rounded normalised head in LDS to `y` (bf16); frequency
+// index j rotates at rope_freq_pos(rp, j) (the row's position, or its mRoPE
+// stream).
 template <int D>
-__device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restrict__ y, int rot, float pos,
+__device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restrict__ y, int rot, const RowPos& rp,
                                               float theta) {
   constexpr int E = D / 64;
   const int lane = threadIdx.x & 63;
@@ -62,7 +64,7 @@ __device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restri
     if (d < rot) {
       const int dd = d < half ? d : d - half;                 // frequency index
       const float freq = 1.0f / powf(theta, (2.0f * dd) / static_cast<float>(rot));
-      const float ang = pos * freq;
+      const float ang = rope_freq_pos(rp, dd) * freq;
       const float c = cosf(ang), s = sinf(ang);
       r = d < half ? s_row[d] * c - s_row[d + half] * s : s_row[d] * c + s_row[d - half] * s;
     }
@@ -75,11 +77,12 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(
     const bf16* __restrict__ q_in, int q_in_stride, bf16* __restrict__ q_out, bf16* __restrict__ gate_out,
     bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ qn_w,
     const bf16* __restrict__ kn_w, bf16* __restrict__ k_cache, bf16* __restrict__ v_cache, int Hq, int Hkv,
-    int max_seq, int rot, float theta, float eps, int pos, const int* __restrict__ positions) {
+    int max_seq, int rot, float theta, float eps, int pos, const int* __restrict__ positions, RopePos ropep) {
   __shared__ float s_row[D];
   const int hh = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
   const int p = positions ? positions[b] : pos;
+  const RowPos rp = rope_row_pos(ropep, b, p);
   if (hh < Hq) {
     const bf16* src = q_in + (static_cast<size_t>(b) * Hq + hh) * q_in_stride;
     bf16* dst = q_out + (static_cast<size_t>(b) * Hq + hh) * D;
@@ -89,14 +92,14 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(
     }
     norm_head_to_lds<D>(src, qn_w, eps, s_row);
     __syncthreads();
-    rope_from_lds<D>(s_row, dst, rot, static_cast<float>(p), theta);
+    rope_from_lds<D>(s_row, dst, rot, rp, theta);
     return;
   }
   const int h = hh - Hq;
   bf16* kr = k + (static_cast<size_t>(b) * Hkv + h) * D;
   norm_head_to_lds<D>(kr, kn_w, eps, s_row);
   __syncthreads();
-  rope_from_lds<D>(s_row, kr, rot, static_cast<float>(p), theta);
+  rope_from_lds<D>(s_row, kr, rot, rp, theta);
   if (k_cache && p >= 0 && p < max_seq) {
     // each lane re-reads only the elements it wrote itself
     const size_t row = ((static_cast<size_t>(b) * Hkv + h) * max_seq + p) * D;
@@ -122,17 +125,18 @@ __global__ __launch_bounds__(64) void head_rms_norm_kernel(bf16* __restrict__ x,
 }
 
 // apply_rope over [S, H, D] rows of q (heads [0, Hq)) and k (heads
-// [Hq, Hq+Hkv)), position start_pos + s: one wave per (head, token).
+// [Hq, Hq+Hkv)), the token of cache row start_pos + s: one wave per
+// (head, token).
 template <int D>
 __global__ __launch_bounds__(64) void rope_kernel(bf16* __restrict__ q, bf16* __restrict__ k, int Hq, int Hkv,
-                                                 int start_pos, int rot, float theta) {
+                                                 int start_pos, int rot, float theta, RopePos ropep) {
   __shared__ float s_row[D];
   const int hh = blockIdx.x, s = blockIdx.y;
   bf16* row = hh < Hq ? q + (static_cast<size_t>(s) * Hq + hh) * D : k + (static_cast<size_t>(s) * Hkv + hh - Hq) * D;
   const int lane = threadIdx.x;
   for (int d = lane; d < D; d += 64) s_row[d] = bf2f(row[d]);
   __syncthreads();
-  rope_from_lds<D>(s_row, row, rot, static_cast<float>(start_pos + s), theta);
+  rope_from_lds<D>(s_row, row, rot, rope_row_pos(ropep, 0, start_pos + s), theta);
 }
 
 // o = in * sigmoid(g), 8 elements per thread where n allows.
@@ -182,8 +186,11 @@ extern "C" int aila_hip_decode_prepare_qkv(const void* q_in, int packed_gate, vo
                                            void* k, const void* v, const void* q_norm_w, const void* k_norm_w,
                                            void* k_cache, void* v_cache, int B, int Hq, int Hkv, int D,
                                            int max_seq, int rotary_dim, float theta, float eps, int pos,
-                                           const int* positions, void* stream) {
+                                           const int* positions, const aila_hip_rope_pos* rope_pos,
+                                           void* stream) {
   using namespace aila;
+  RopePos rpd;
+  if (int rc = load_rope_pos(rope_pos, &rpd, "decode_prepare_qkv")) return rc;
   AILA_REQUIRE(q_in && q_out && k && v, "decode_prepare_qkv: null pointer");
   AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "decode_prepare_qkv: bad shape (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
@@ -202,7 +209,7 @@ extern "C" int aila_hip_decode_prepare_qkv(const void* q_in, int packed_gate, vo
                        packed_gate ? static_cast<bf16*>(gate_out) : nullptr, static_cast<bf16*>(k),
                        static_cast<const bf16*>(v), static_cast<const bf16*>(q_norm_w),
                        static_cast<const bf16*>(k_norm_w), static_cast<bf16*>(k_cache),
-                       static_cast<bf16*>(v_cache), Hq, Hkv, max_seq, rot, theta, eps, pos, positions);
+                       static_cast<bf16*>(v_cache), Hq, Hkv, max_seq, rot, theta, eps, pos, positions, rpd);
     return check_launch("decode_prepare_qkv");
   });
 }
@@ -225,10 +232,12 @@ extern "C" int aila_hip_head_rms_norm(void* x, const void* weight, int S, int H,
 }
 
 extern "C" int aila_hip_apply_rope(void* q, void* k, int S, int start_pos, int Hq, int Hkv, int D, int rotary_dim,
-                                   float theta, void* stream) {
+                                   float theta, const aila_hip_rope_pos* rope_pos, void* stream) {
   using namespace aila;
   AILA_REQUIRE(q && k, "apply_rope: null pointer");
-  AILA_REQUIRE(S >= 0 && S <= 65535 && start_pos >= 0 && Hq > 0 && Hkv > 0 && theta > 0.f,
+  RopePos rpd;
+  if (int rc = load_rope_pos(rope_pos, &rpd, "apply_rope")) return rc;
+  AILA_REQUIRE(S >= 0 && S <= 65535 && start_pos >= 0 && Hq > 0 && Hkv > 0 && Hkv <= Hq && theta > 0.f,
                "apply_rope: bad shape (S=%d start_pos=%d Hq=%d Hkv=%d)", S, start_pos, Hq, Hkv);
   if (S == 0) return AILA_HIP_OK;
   const int rot = clamp_rot(D, rotary_dim);
@@ -236,7 +245,7 @@ extern "C" int aila_hip_apply_rope(void* q, void* k, int S, int start_pos, int H
   return with_d(D, "apply_rope", [&](auto dc) {
     constexpr int DD = decltype(dc)::value;
     hipLaunchKernelGGL((rope_kernel<DD>), dim3(Hq + Hkv, S), dim3(64), 0, st, static_cast<bf16*>(q),
-                       static_cast<bf16*>(k), Hq, Hkv, start_pos, rot, theta);
+                       static_cast<bf16*>(k), Hq, Hkv, start_pos, rot, theta, rpd);
     return check_launch("apply_rope");
   });
 }

@@ -63,6 +63,7 @@ struct PrepArgs {
   int apply_gate;        // packed only: out *= sigmoid(gate) instead of copying the gate out
   int rot;               // rotary dims, even, in [2, D]
   float theta, eps;
+  RopePos rope;          // rotary positions (zero: the cache row)
 };
 
 // Paged KV cache: the rows of sequence b live in fixed-size pages of a
@@ -200,10 +201,11 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     // Prepared q, computed once per workgroup: wave w normalises heads w and
     // w + 4 (one wave per head, D/64 dims per lane), the RoPE pass rotates
     // pairs in place, and every wave then reads its A operands from LDS.
-    const int p = len - 1, half = pa.rot / 2;
+    const int half = pa.rot / 2;
+    const RowPos rp = rope_row_pos(pa.rope, b, len - 1);
     for (int j = threadIdx.x; j < half; j += kThreads) {
       const float freq = 1.0f / powf(pa.theta, (2.0f * j) / static_cast<float>(pa.rot));
-      const float ang = static_cast<float>(p) * freq;
+      const float ang = rope_freq_pos(rp, j) * freq;
       s_tab[2 * j] = cosf(ang);
       s_tab[2 * j + 1] = sinf(ang);
     }
@@ -846,7 +848,8 @@ extern "C" int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_g
                                                   const void* k_norm_w, void* k_cache, void* v_cache, void* out,
                                                   void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
                                                   int D, int max_seq, int rotary_dim, float theta, float eps,
-                                                  int pos, const int* positions, void* stream) {
+                                                  int pos, const int* positions,
+                                                  const aila_hip_rope_pos* rope_pos, void* stream) {
   using namespace aila;
   AILA_REQUIRE(k_new && v_new, "gqa_decode_prepare_append: null k_new/v_new");
   AILA_REQUIRE(packed_gate >= 0 && packed_gate <= 2, "gqa_decode_prepare_append: packed_gate=%d not 0, 1 or 2",
@@ -866,6 +869,7 @@ extern "C" int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_g
   pa.rot = rot;
   pa.theta = theta;
   pa.eps = eps;
+  if (int rc = load_rope_pos(rope_pos, &pa.rope, "gqa_decode_prepare_append")) return rc;
   return gqa_decode_impl(q_in, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, pos + 1,
                          positions, 1, k_new, v_new, static_cast<hipStream_t>(stream), &pa);
 }

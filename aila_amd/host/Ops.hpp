@@ -101,7 +101,11 @@ void sigmoid_mul(Context& ctx, Tensor& input, Tensor& gate, Tensor& output, int 
 
 // NeoX RoPE in place over the full head (Ops.hpp:175-178) and over the first
 // rotary_dim dims (Ops.hpp:181-194); rotary_dim is clamped to [2, head_dim]
-// and made even. text_pos_delta shifts positions >= prompt_pos_len.
+// and made even. text_pos_delta shifts positions >= prompt_pos_len; with
+// interleaved and all three of pos_t/pos_h/pos_w (device int arrays indexed by
+// position) the frequency pairs take the mRoPE streams (ElementwiseOps.cpp:60-78).
+// The decode-prepare ops below take the same arguments; their cache row stays
+// start_pos.
 void apply_rope(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,
                 int num_kv_heads, int head_dim, float theta);
 void apply_rope_partial(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,

@@ -154,16 +154,23 @@ namespace {
 
 void* opt(Tensor& t) { return t.valid() ? t.data() : nullptr; }
 
-void no_mrope(bool interleaved, const int* pos_t, const int* pos_h, const int* pos_w, const char* what) {
-  if (interleaved && pos_t && pos_h && pos_w)
-    throw std::runtime_error(std::string(what) + ": interleaved mRoPE position streams are not supported");
-}
-
-// The decode ops rotate and append at one position; a text shift that would
-// separate the two is refused.
-void no_decode_shift(int start_pos, int prompt_pos_len, int text_pos_delta, const char* what) {
-  if (text_pos_delta != 0 && start_pos >= prompt_pos_len)
-    throw std::runtime_error(std::string(what) + ": text_pos_delta is not supported");
+// The reference's rotary position arguments (ElementwiseOps.cpp:33-103,
+// 555-863) as the C ABI's position record. The position streams are the
+// engine's device arrays, indexed by cache row.
+aila_hip_rope_pos rope_pos(bool interleaved, const int* pos_t, const int* pos_h, const int* pos_w,
+                           int prompt_pos_len, int text_pos_delta, int sec_t, int sec_h, int sec_w) {
+  aila_hip_rope_pos rp{};
+  rp.interleaved = interleaved ? 1 : 0;
+  rp.pos_t = pos_t;
+  rp.pos_h = pos_h;
+  rp.pos_w = pos_w;
+  rp.pos_stride = 0;
+  rp.prompt_pos_len = prompt_pos_len;
+  rp.text_pos_delta = text_pos_delta;
+  rp.mrope_section_t = sec_t;
+  rp.mrope_section_h = sec_h;
+  rp.mrope_section_w = sec_w;
+  return rp;
 }
 
 }  // namespace
@@ -191,27 +198,14 @@ void apply_rope(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, 
 void apply_rope_partial(Context& ctx, Tensor& q, Tensor& k, int seq_len, int start_pos, int num_heads_q,
                         int num_kv_heads, int head_dim, int rotary_dim, float theta, bool interleaved,
                         const int* pos_t, const int* pos_h, const int* pos_w, int prompt_pos_len,
-                        int text_pos_delta, int, int, int) {
-  no_mrope(interleaved, pos_t, pos_h, pos_w, "apply_rope_partial");
+                        int text_pos_delta, int mrope_section_t, int mrope_section_h, int mrope_section_w) {
   need_dtype(q, DType::bf16, "apply_rope q");
   need_dtype(k, DType::bf16, "apply_rope k");
-  // rows before prompt_pos_len rotate at their own position, the rest at
-  // position + text_pos_delta (ElementwiseOps.cpp:54-58)
-  int unshifted = text_pos_delta == 0 ? seq_len : std::max(0, std::min(seq_len, prompt_pos_len - start_pos));
-  char* qp = static_cast<char*>(q.data());
-  char* kp = static_cast<char*>(k.data());
-  if (unshifted > 0)
-    check(aila_hip_apply_rope(qp, kp, unshifted, start_pos, num_heads_q, num_kv_heads, head_dim, rotary_dim,
-                              theta, ctx.stream()),
-          "apply_rope_partial");
-  if (unshifted < seq_len) {
-    const size_t qrow = static_cast<size_t>(num_heads_q) * head_dim * 2;
-    const size_t krow = static_cast<size_t>(num_kv_heads) * head_dim * 2;
-    check(aila_hip_apply_rope(qp + unshifted * qrow, kp + unshifted * krow, seq_len - unshifted,
-                              start_pos + unshifted + text_pos_delta, num_heads_q, num_kv_heads, head_dim,
-                              rotary_dim, theta, ctx.stream()),
-          "apply_rope_partial");
-  }
+  const aila_hip_rope_pos rp = rope_pos(interleaved, pos_t, pos_h, pos_w, prompt_pos_len, text_pos_delta,
+                                        mrope_section_t, mrope_section_h, mrope_section_w);
+  check(aila_hip_apply_rope(q.data(), k.data(), seq_len, start_pos, num_heads_q, num_kv_heads, head_dim, rotary_dim,
+                            theta, &rp, ctx.stream()),
+        "apply_rope_partial");
 }
 
 void decode_prepare_qkv(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& rope_freq,
@@ -227,14 +221,15 @@ void decode_prepare_qkv_partial(Context& ctx, Tensor& q, Tensor& k, Tensor& v, T
                                 Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache, int start_pos,
                                 int num_heads_q, int num_kv_heads, int head_dim, float eps, int rotary_dim,
                                 float theta, bool interleaved, const int* pos_t, const int* pos_h,
-                                const int* pos_w, int prompt_pos_len, int text_pos_delta, int, int, int) {
-  no_mrope(interleaved, pos_t, pos_h, pos_w, "decode_prepare_qkv_partial");
-  no_decode_shift(start_pos, prompt_pos_len, text_pos_delta, "decode_prepare_qkv_partial");
+                                const int* pos_w, int prompt_pos_len, int text_pos_delta, int mrope_section_t,
+                                int mrope_section_h, int mrope_section_w) {
+  const aila_hip_rope_pos rp = rope_pos(interleaved, pos_t, pos_h, pos_w, prompt_pos_len, text_pos_delta,
+                                        mrope_section_t, mrope_section_h, mrope_section_w);
   for (Tensor* t : {&q, &k, &v, &k_cache, &v_cache}) need_dtype(*t, DType::bf16, "decode_prepare_qkv");
   check(aila_hip_decode_prepare_qkv(q.data(), 0, q.data(), nullptr, k.data(), v.data(), opt(q_norm_weight),
                                     opt(k_norm_weight), k_cache.data(), v_cache.data(), 1, num_heads_q,
                                     num_kv_heads, head_dim, static_cast<int>(k_cache.shape(1)), rotary_dim,
-                                    theta, eps, start_pos, nullptr, ctx.stream()),
+                                    theta, eps, start_pos, nullptr, &rp, ctx.stream()),
         "decode_prepare_qkv");
 }
 
@@ -244,15 +239,16 @@ void decode_prepare_qgkv_packed_partial(Context& ctx, Tensor& q_gate_packed, Ten
                                         int start_pos, int num_heads_q, int num_kv_heads, int head_dim,
                                         float eps, int rotary_dim, float theta, bool interleaved,
                                         const int* pos_t, const int* pos_h, const int* pos_w,
-                                        int prompt_pos_len, int text_pos_delta, int, int, int) {
-  no_mrope(interleaved, pos_t, pos_h, pos_w, "decode_prepare_qgkv_packed_partial");
-  no_decode_shift(start_pos, prompt_pos_len, text_pos_delta, "decode_prepare_qgkv_packed_partial");
+                                        int prompt_pos_len, int text_pos_delta, int mrope_section_t,
+                                        int mrope_section_h, int mrope_section_w) {
+  const aila_hip_rope_pos rp = rope_pos(interleaved, pos_t, pos_h, pos_w, prompt_pos_len, text_pos_delta,
+                                        mrope_section_t, mrope_section_h, mrope_section_w);
   for (Tensor* t : {&q_gate_packed, &k, &v, &q_out, &gate_out, &k_cache, &v_cache})
     need_dtype(*t, DType::bf16, "decode_prepare_qgkv_packed_partial");
   check(aila_hip_decode_prepare_qkv(q_gate_packed.data(), 1, q_out.data(), gate_out.data(), k.data(), v.data(),
                                     opt(q_norm_weight), opt(k_norm_weight), k_cache.data(), v_cache.data(), 1,
                                     num_heads_q, num_kv_heads, head_dim, static_cast<int>(k_cache.shape(1)),
-                                    rotary_dim, theta, eps, start_pos, nullptr, ctx.stream()),
+                                    rotary_dim, theta, eps, start_pos, nullptr, &rp, ctx.stream()),
         "decode_prepare_qgkv_packed_partial");
 }
 

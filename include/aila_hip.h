@@ -36,6 +36,38 @@ const char* aila_hip_last_error(void);
 /* ABI version: (major << 16) | minor. */
 int aila_hip_version(void);
 
+/* Rotary positions of a token when they differ from its cache row: the text
+ * position shift and the interleaved multimodal RoPE (mRoPE) streams of
+ * ops::apply_rope_partial / decode_prepare_qkv_partial /
+ * decode_prepare_qgkv_packed_partial (src/ops/ElementwiseOps.cpp:33-103,
+ * 555-863). For the token in cache row r of sequence b, with
+ * P = prompt_pos_lens ? prompt_pos_lens[b] : prompt_pos_len and
+ * delta = text_pos_deltas ? text_pos_deltas[b] : text_pos_delta:
+ *   scalar = r >= P ? r + delta : r                       (:54-58)
+ * and frequency index d (0 <= d < rotary_dim/2) rotates at `scalar`, or, when
+ * `interleaved` is nonzero and pos_t, pos_h and pos_w are all given, at
+ *   h-stream if d % 3 == 1 and d / 3 < mrope_section_h,
+ *   w-stream if d % 3 == 2 and d / 3 < mrope_section_w,
+ *   t-stream otherwise                                    (:60-78)
+ * where a stream's value is pos_X[b * pos_stride + r] for r < P and `scalar`
+ * past the prompt. pos_t/pos_h/pos_w are device int arrays holding at least
+ * P entries per sequence; mrope_section_t is accepted and, as in the
+ * reference, unused. A zero-initialised struct (or a NULL pointer where an
+ * entry point takes one) means "rotate at the cache row". The cache row a
+ * decode step appends to is never shifted. */
+typedef struct aila_hip_rope_pos {
+  int interleaved;
+  const int* pos_t;
+  const int* pos_h;
+  const int* pos_w;
+  int pos_stride;
+  int prompt_pos_len;
+  int text_pos_delta;
+  const int* prompt_pos_lens; /* optional device int[B] */
+  const int* text_pos_deltas; /* optional device int[B] */
+  int mrope_section_t, mrope_section_h, mrope_section_w;
+} aila_hip_rope_pos;
+
 /* ---------------------------------------------------------------- GQA --- */
 
 /* Workspace bytes needed by aila_hip_gqa_decode for up to B sequences of
@@ -148,8 +180,10 @@ int aila_hip_gqa_decode_append(const void* q, const void* k_new,
  *   [B, Hkv, D]; q_norm_w/k_norm_w [D] bf16 or NULL (weight 1). The prepared
  *   k and v_new go to cache row pos (or positions[b]) and sequence b attends
  *   rows [0, row]; q_in and k_new are not modified (the prepared q lives only
- *   in LDS). rotary_dim is clamped to [2, D] and made even. Other arguments
- *   as aila_hip_gqa_decode. */
+ *   in LDS). rotary_dim is clamped to [2, D] and made even. rope_pos (NULL =
+ *   rotate at the cache row) gives the text shift / mRoPE positions of
+ *   aila_hip_rope_pos; the new row is still written at the cache row. Other
+ *   arguments as aila_hip_gqa_decode. */
 int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_gate,
                                        void* gate_out, const void* k_new,
                                        const void* v_new, const void* q_norm_w,
@@ -159,6 +193,7 @@ int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_gate,
                                        int B, int Hq, int Hkv, int D,
                                        int max_seq, int rotary_dim, float theta,
                                        float eps, int pos, const int* positions,
+                                       const aila_hip_rope_pos* rope_pos,
                                        void* stream);
 
 /* Append one decoded token's K and V per sequence to the cache (the
@@ -349,8 +384,9 @@ int aila_hip_deltanet_prefill(const void* q, const void* k, const void* v,
  * Replaces ops::decode_prepare_qkv (src/ops/ElementwiseOps.cpp:105-216),
  * ops::decode_prepare_qkv_partial (:555-705) and
  * ops::decode_prepare_qgkv_packed_partial (:707-863, packed_gate != 0) for
- * text positions (no mRoPE); rounding points as the reference (bf16 after
- * the norm and after the rotation).
+ * the cache row as the position, or the shifted / mRoPE positions of
+ * rope_pos (NULL = the cache row); rounding points as the reference (bf16
+ * after the norm and after the rotation).
  *   q_in     [B, Hq, D] bf16, or [B, Hq, 2D] (q | gate per head) if packed_gate
  *   q_out    [B, Hq, D] bf16 (may equal q_in when not packed)
  *   gate_out [B, Hq, D] bf16, the gate half copied through (packed_gate only)
@@ -363,19 +399,23 @@ int aila_hip_decode_prepare_qkv(const void* q_in, int packed_gate, void* q_out, 
                                 void* k, const void* v, const void* q_norm_w, const void* k_norm_w,
                                 void* k_cache, void* v_cache, int B, int Hq, int Hkv, int D,
                                 int max_seq, int rotary_dim, float theta, float eps, int pos,
-                                const int* positions, void* stream);
+                                const int* positions, const aila_hip_rope_pos* rope_pos,
+                                void* stream);
 
 /* Per-head RMSNorm in place over x [S, H, D] bf16 with weight [D] bf16 (NULL
  * = 1). Replaces ops::head_rms_norm (src/ops/NormOps.cpp:277-321).
  * Supported: D in {64, 128, 256}. */
 int aila_hip_head_rms_norm(void* x, const void* weight, int S, int H, int D, float eps, void* stream);
 
-/* RoPE in place on q [S, Hq, D] and k [S, Hkv, D] bf16 at positions
- * start_pos + s, NeoX half-split over the first rotary_dim dims. Replaces
- * ops::apply_rope / apply_rope_partial for text positions
- * (src/ops/ElementwiseOps.cpp:33-103). Supported: D in {64, 128, 256}. */
+/* RoPE in place on q [S, Hq, D] and k [S, Hkv, D] bf16, NeoX half-split
+ * over the first rotary_dim dims; row s is the token in cache row
+ * start_pos + s, rotated at that row or at the positions rope_pos gives for
+ * it (sequence 0 of aila_hip_rope_pos; NULL = the row). Replaces
+ * ops::apply_rope / apply_rope_partial, including the text shift and the
+ * interleaved mRoPE streams (src/ops/ElementwiseOps.cpp:33-103).
+ * Supported: D in {64, 128, 256}, Hkv <= Hq. */
 int aila_hip_apply_rope(void* q, void* k, int S, int start_pos, int Hq, int Hkv, int D, int rotary_dim,
-                        float theta, void* stream);
+                        float theta, const aila_hip_rope_pos* rope_pos, void* stream);
 
 /* output = input * sigmoid(gate), n bf16 elements (output may equal input).
  * Replaces ops::sigmoid_mul (src/ops/ElementwiseOps.cpp:519-553), the

@@ -37,6 +37,10 @@ _SIGS = {
     "orc_attention_f64": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "orc_head_rms_norm": [_P, _P, _P, _F, _I, _I, _I],
     "orc_apply_rope": [_P, _P, _I, _I, _I, _I, _I, _I, _F],
+    "orc_apply_rope_partial": [_P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _I, _I, _I, _I, _I],
+    "orc_decode_prepare_rp": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                              _I, _I, _I, _I, _I, _I, _F, _F, _P,
+                              _I, _P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _I],
     "orc_decode_prepare_qkv": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _I],
     "orc_decode_prepare": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                            _I, _I, _I, _I, _I, _I, _F, _F, _P],
@@ -147,10 +151,35 @@ def head_rms_norm(x, eps, S, H, D, w_bf16=None, w_f32=None):
     return x
 
 
-def apply_rope(q, k, S, start_pos, Hq, Hkv, D, rotary_dim, theta):
+def _rope_fields(rope):
+    """Unpack a rotary-position dict: interleaved, pos_t/pos_h/pos_w (int
+    arrays [P] or [B, P]), prompt_pos_len, text_pos_delta, prompt_lens and
+    deltas (int [B]), sections (t, h, w)."""
+    rope = rope or {}
+    streams = [rope.get(n) for n in ("pos_t", "pos_h", "pos_w")]
+    streams = [None if a is None else np.ascontiguousarray(a, dtype=np.int32) for a in streams]
+    stride = 0
+    if streams[0] is not None and streams[0].ndim == 2:
+        stride = streams[0].shape[1]
+    pl, dl = rope.get("prompt_lens"), rope.get("deltas")
+    pl = None if pl is None else np.ascontiguousarray(pl, dtype=np.int32)
+    dl = None if dl is None else np.ascontiguousarray(dl, dtype=np.int32)
+    sec = tuple(int(x) for x in rope.get("sections", (0, 0, 0)))
+    return (int(bool(rope.get("interleaved", True))), streams, stride, int(rope.get("prompt_pos_len", 0)),
+            int(rope.get("text_pos_delta", 0)), pl, dl, sec)
+
+
+def apply_rope(q, k, S, start_pos, Hq, Hkv, D, rotary_dim, theta, rope=None):
+    """apply_rope_partial; ``rope`` (dict, see _rope_fields) gives the text
+    shift and mRoPE streams (one sequence: streams [P])."""
     q = np.array(q, dtype=U16, copy=True, order="C")
     k = np.array(k, dtype=U16, copy=True, order="C")
-    lib().orc_apply_rope(_p(q), _p(k), S, start_pos, Hq, Hkv, D, rotary_dim, theta)
+    if rope is None:
+        lib().orc_apply_rope(_p(q), _p(k), S, start_pos, Hq, Hkv, D, rotary_dim, theta)
+        return q, k
+    il, (pt, ph, pw), _, plen, delta, _, _, sec = _rope_fields(rope)
+    lib().orc_apply_rope_partial(_p(q), _p(k), S, start_pos, Hq, Hkv, D, rotary_dim, theta, il, _p(pt), _p(ph),
+                                 _p(pw), plen, delta, *sec)
     return q, k
 
 
@@ -165,9 +194,11 @@ def decode_prepare_qkv(q, k, v, qn_w, kn_w, kc, vc, start_pos, Hq, Hkv, D, eps, 
 
 
 def decode_prepare(q_in, k, v, qn_w, kn_w, kc, vc, pos, B, Hq, Hkv, D, max_seq, rotary_dim,
-                   theta, eps, packed=False):
+                   theta, eps, packed=False, rope=None):
     """Batched decode_prepare_qkv(_partial / qgkv_packed). Returns
-    (q_out, gate_out or None, k); kc/vc (uint16 arrays or None) are updated."""
+    (q_out, gate_out or None, k); kc/vc (uint16 arrays or None) are updated.
+    ``rope``: rotary positions as in apply_rope (streams [P] shared or
+    [B, P] per sequence; prompt_lens/deltas per sequence)."""
     q_in = _c(q_in, U16)
     k = np.array(k, dtype=U16, copy=True, order="C")
     v, qn_w, kn_w = _c(v, U16), _c(qn_w, U16), _c(kn_w, U16)
@@ -176,9 +207,11 @@ def decode_prepare(q_in, k, v, qn_w, kn_w, kc, vc, pos, B, Hq, Hkv, D, max_seq, 
     posa = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (B,)))
     if kc is not None:
         assert kc.dtype == U16 and vc.dtype == U16 and kc.flags.c_contiguous
-    lib().orc_decode_prepare(_p(q_in), int(bool(packed)), _p(q_out), _p(gate), _p(k), _p(v), _p(qn_w),
-                             _p(kn_w), _p(kc), _p(vc), B, Hq, Hkv, D, max_seq, rotary_dim, theta, eps,
-                             _p(posa))
+    il, (pt, ph, pw), stride, plen, delta, pl, dl, sec = _rope_fields(rope)
+    lib().orc_decode_prepare_rp(_p(q_in), int(bool(packed)), _p(q_out), _p(gate), _p(k), _p(v), _p(qn_w),
+                                _p(kn_w), _p(kc), _p(vc), B, Hq, Hkv, D, max_seq, rotary_dim, theta, eps,
+                                _p(posa), il if rope else 0, _p(pt), _p(ph), _p(pw), stride, plen, delta,
+                                _p(pl), _p(dl), *sec)
     return q_out, gate, k
 
 

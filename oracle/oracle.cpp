@@ -412,18 +412,41 @@ void orc_head_rms_norm(bf16_t* x, const bf16_t* w_bf16, const float* w_f32,
   }
 }
 
-// apply_rope_partial (non-interleaved, no mRoPE), ElementwiseOps.cpp:33-103:
-// NeoX half-split rotation of the first `rot` dims of every head, position
-// start_pos + s, freq = 1 / theta^(2d/rot); q and k rounded to bf16.
-void orc_apply_rope(bf16_t* q, bf16_t* k, int S, int start_pos, int Hq,
-                    int Hkv, int D, int rotary_dim, float theta) {
+// apply_rope_partial, ElementwiseOps.cpp:33-103: NeoX half-split rotation of
+// the first `rot` dims of every head for the token at global position
+// start_pos + s; freq = 1 / theta^(2d/rot); q and k rounded to bf16. The
+// rotary position is the global position, shifted by text_pos_delta past
+// prompt_pos_len (:54-58); with `interleaved` and all three streams, pair d
+// takes the h stream when d%3 == 1 and d/3 < sec_h, the w stream when
+// d%3 == 2 and d/3 < sec_w, else the t stream, each read at the global
+// position inside the prompt and equal to the shifted scalar past it
+// (:60-78). sec_t is unused, as in the reference. The k rows rotate in the
+// same pass for heads h < Hkv of the q-head loop.
+void orc_apply_rope_partial(bf16_t* q, bf16_t* k, int S, int start_pos, int Hq, int Hkv, int D,
+                            int rotary_dim, float theta, int interleaved, const int* pos_t,
+                            const int* pos_h, const int* pos_w, int prompt_pos_len,
+                            int text_pos_delta, int sec_t, int sec_h, int sec_w) {
+  (void)sec_t;
   int rot = std::max(2, std::min(D, rotary_dim));
   if (rot & 1) --rot;
   const int half = rot / 2;
   for (int s = 0; s < S; ++s)
     for (int h = 0; h < Hq; ++h)
       for (int d = 0; d < half; ++d) {
-        const float pos = static_cast<float>(start_pos + s);
+        const int global_pos = start_pos + s;
+        int pos_scalar = global_pos;
+        if (global_pos >= prompt_pos_len) pos_scalar = global_pos + text_pos_delta;
+        float pos = static_cast<float>(pos_scalar);
+        if (interleaved && pos_t && pos_h && pos_w) {
+          int stream = 0;
+          if ((d % 3) == 1 && (d / 3) < sec_h) stream = 1;
+          else if ((d % 3) == 2 && (d / 3) < sec_w) stream = 2;
+          const bool in_prompt = global_pos < prompt_pos_len;
+          const int t_val = in_prompt ? pos_t[global_pos] : pos_scalar;
+          const int h_val = in_prompt ? pos_h[global_pos] : pos_scalar;
+          const int w_val = in_prompt ? pos_w[global_pos] : pos_scalar;
+          pos = static_cast<float>(stream == 1 ? h_val : stream == 2 ? w_val : t_val);
+        }
         const float freq = 1.0f / std::pow(theta, (2.0f * d) / static_cast<float>(rot));
         const float ang = pos * freq;
         const float c = std::cos(ang), sn = std::sin(ang);
@@ -438,6 +461,13 @@ void orc_apply_rope(bf16_t* q, bf16_t* k, int S, int start_pos, int Hq,
           kr[d + half] = orc_f32_to_bf16(k1 * c + k0 * sn);
         }
       }
+}
+
+// Text positions only (no shift, no streams): position start_pos + s.
+void orc_apply_rope(bf16_t* q, bf16_t* k, int S, int start_pos, int Hq,
+                    int Hkv, int D, int rotary_dim, float theta) {
+  orc_apply_rope_partial(q, k, S, start_pos, Hq, Hkv, D, rotary_dim, theta, 0, nullptr, nullptr, nullptr, 0, 0,
+                         0, 0, 0);
 }
 
 // decode_prepare_qkv, ElementwiseOps.cpp:105-216 (full rotary, one token):
@@ -457,17 +487,23 @@ void orc_decode_prepare_qkv(bf16_t* q, bf16_t* k, const bf16_t* v,
 }
 
 // decode_prepare_qkv_partial (ElementwiseOps.cpp:555-705) and
-// decode_prepare_qgkv_packed_partial (:707-863), text positions, batched over
-// B independent sequences (the reference runs one): per head, q (the first
-// D of a packed [q | gate] head when packed, gate copied through) and k get
-// RMSNorm (bf16 round) then RoPE over the first `rot` dims at pos[b]
-// (bf16 round); k, v are appended to the cache row pos[b] when kc != null.
+// decode_prepare_qgkv_packed_partial (:707-863), batched over B independent
+// sequences (the reference runs one): per head, q (the first D of a packed
+// [q | gate] head when packed, gate copied through) and k get RMSNorm (bf16
+// round) then RoPE over the first `rot` dims for the token at global position
+// pos[b] (bf16 round; the rotary_position lambda, :593-617, is
+// apply_rope_partial's position rule at that one position); k, v are appended
+// to the cache row pos[b] when kc != null.
 // q_in [B,Hq,D or 2D]; q_out, gate_out [B,Hq,D]; k (in place), v [B,Hkv,D];
-// kc, vc [B,Hkv,max_seq,D].
-void orc_decode_prepare(const bf16_t* q_in, int packed, bf16_t* q_out, bf16_t* gate_out, bf16_t* k,
-                        const bf16_t* v, const bf16_t* qn_w, const bf16_t* kn_w, bf16_t* kc, bf16_t* vc,
-                        int B, int Hq, int Hkv, int D, int max_seq, int rotary_dim, float theta,
-                        float eps, const int* pos) {
+// kc, vc [B,Hkv,max_seq,D]. Rotary positions: sequence b reads its streams
+// at pos_t/h/w + b*pos_stride, its prompt length and text delta from
+// prompt_lens[b] / deltas[b] when given, else the scalars.
+void orc_decode_prepare_rp(const bf16_t* q_in, int packed, bf16_t* q_out, bf16_t* gate_out, bf16_t* k,
+                           const bf16_t* v, const bf16_t* qn_w, const bf16_t* kn_w, bf16_t* kc, bf16_t* vc,
+                           int B, int Hq, int Hkv, int D, int max_seq, int rotary_dim, float theta,
+                           float eps, const int* pos, int interleaved, const int* pos_t, const int* pos_h,
+                           const int* pos_w, int pos_stride, int prompt_pos_len, int text_pos_delta,
+                           const int* prompt_lens, const int* deltas, int sec_t, int sec_h, int sec_w) {
   const int qs = packed ? 2 * D : D;
   for (int b = 0; b < B; ++b) {
     bf16_t* qo = q_out + static_cast<size_t>(b) * Hq * D;
@@ -480,7 +516,11 @@ void orc_decode_prepare(const bf16_t* q_in, int packed, bf16_t* q_out, bf16_t* g
     bf16_t* kb = k + static_cast<size_t>(b) * Hkv * D;
     orc_head_rms_norm(qo, qn_w, nullptr, eps, 1, Hq, D);
     orc_head_rms_norm(kb, kn_w, nullptr, eps, 1, Hkv, D);
-    orc_apply_rope(qo, kb, 1, pos[b], Hq, Hkv, D, rotary_dim, theta);
+    const size_t off = static_cast<size_t>(b) * pos_stride;
+    orc_apply_rope_partial(qo, kb, 1, pos[b], Hq, Hkv, D, rotary_dim, theta, interleaved,
+                           pos_t ? pos_t + off : nullptr, pos_h ? pos_h + off : nullptr,
+                           pos_w ? pos_w + off : nullptr, prompt_lens ? prompt_lens[b] : prompt_pos_len,
+                           deltas ? deltas[b] : text_pos_delta, sec_t, sec_h, sec_w);
     if (kc) {
       for (int h = 0; h < Hkv; ++h) {
         const size_t row = ((static_cast<size_t>(b) * Hkv + h) * max_seq + pos[b]) * D;
@@ -491,6 +531,16 @@ void orc_decode_prepare(const bf16_t* q_in, int packed, bf16_t* q_out, bf16_t* g
       }
     }
   }
+}
+
+// The same at text positions (rotary position = cache row).
+void orc_decode_prepare(const bf16_t* q_in, int packed, bf16_t* q_out, bf16_t* gate_out, bf16_t* k,
+                        const bf16_t* v, const bf16_t* qn_w, const bf16_t* kn_w, bf16_t* kc, bf16_t* vc,
+                        int B, int Hq, int Hkv, int D, int max_seq, int rotary_dim, float theta,
+                        float eps, const int* pos) {
+  orc_decode_prepare_rp(q_in, packed, q_out, gate_out, k, v, qn_w, kn_w, kc, vc, B, Hq, Hkv, D, max_seq,
+                        rotary_dim, theta, eps, pos, 0, nullptr, nullptr, nullptr, 0, 0, 0, nullptr, nullptr, 0,
+                        0, 0);
 }
 
 // sigmoid_mul, ElementwiseOps.cpp:519-553: o = bf16(in * 1/(1+e^-g)).

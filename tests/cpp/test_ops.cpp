@@ -23,6 +23,12 @@ void orc_deltanet_recurrent(const uint16_t*, const uint16_t*, const uint16_t*, c
                             int, int, int, int, int, float, float, int);
 void orc_head_rms_norm(uint16_t*, const uint16_t*, const float*, float, int, int, int);
 void orc_apply_rope(uint16_t*, uint16_t*, int, int, int, int, int, int, float);
+void orc_apply_rope_partial(uint16_t*, uint16_t*, int, int, int, int, int, int, float, int, const int*, const int*,
+                            const int*, int, int, int, int, int);
+void orc_decode_prepare_rp(const uint16_t*, int, uint16_t*, uint16_t*, uint16_t*, const uint16_t*, const uint16_t*,
+                           const uint16_t*, uint16_t*, uint16_t*, int, int, int, int, int, int, float, float,
+                           const int*, int, const int*, const int*, const int*, int, int, int, const int*,
+                           const int*, int, int, int);
 void orc_decode_prepare(const uint16_t*, int, uint16_t*, uint16_t*, uint16_t*, const uint16_t*, const uint16_t*,
                         const uint16_t*, uint16_t*, uint16_t*, int, int, int, int, int, int, float, float,
                         const int*);
@@ -334,14 +340,45 @@ int main() {
     orc_sigmoid_mul(a.data(), g.data(), wa.data(), n);
     e = relerr(download<uint16_t>(ctx, ta), wa);
     expect(e <= 1e-2, "sigmoid_mul", e);
-    bool threw = false;
-    int pt[1] = {0};
-    try {
-      ops::apply_rope_partial(ctx, txq, txk, S, start, Hq, Hkv, D, rot, theta, true, pt, pt, pt, 1, 0, 8, 12, 12);
-    } catch (const std::runtime_error&) {
-      threw = true;
+    // interleaved mRoPE (prompt rows take their t/h/w streams, later rows
+    // the shifted text position), prefill and decode forms
+    {
+      const int P = 30, dshift = -12, sec_t = 11, sec_h = 11, sec_w = 10;
+      std::vector<int> pt(P), ph(P), pw(P);
+      for (int i = 0; i < P; ++i) pt[i] = i / 3, ph[i] = (i * 7) % 11, pw[i] = (i * 5) % 13;
+      Tensor tpt = upload(ctx, pt, {P}, DType::s32), tph = upload(ctx, ph, {P}, DType::s32),
+             tpw = upload(ctx, pw, {P}, DType::s32);
+      u16v mq = rand_bf16(size_t(S) * Hq * D), mk = rand_bf16(size_t(S) * Hkv * D);
+      Tensor tmq = upload(ctx, mq, {S, Hq * D}, DType::bf16), tmk = upload(ctx, mk, {S, Hkv * D}, DType::bf16);
+      ops::apply_rope_partial(ctx, tmq, tmk, S, start, Hq, Hkv, D, rot, theta, true, tpt.data_as<int>(),
+                              tph.data_as<int>(), tpw.data_as<int>(), P, dshift, sec_t, sec_h, sec_w);
+      orc_apply_rope_partial(mq.data(), mk.data(), S, start, Hq, Hkv, D, rot, theta, 1, pt.data(), ph.data(),
+                             pw.data(), P, dshift, sec_t, sec_h, sec_w);
+      e = std::fmax(relerr(download<uint16_t>(ctx, tmq), mq), relerr(download<uint16_t>(ctx, tmk), mk));
+      expect(e <= 1e-2, "apply_rope_partial (interleaved mRoPE + text shift)", e);
+      // decode step inside the prompt (streams) and past it (shift); cache row = start_pos
+      for (const int sp : {P - 4, P + 40}) {
+        u16v dq = rand_bf16(size_t(Hq) * 2 * D), dk = rand_bf16(size_t(Hkv) * D);
+        Tensor tdq = upload(ctx, dq, {1, Hq * 2 * D}, DType::bf16), tdk = upload(ctx, dk, {1, Hkv * D}, DType::bf16);
+        Tensor qo2 = Tensor::allocate(ctx, {1, Hq * D}), go2 = Tensor::allocate(ctx, {1, Hq * D});
+        ops::decode_prepare_qgkv_packed_partial(ctx, tdq, tdk, tv, qo2, go2, tqw, tkw, kc, vc, sp, Hq, Hkv, D, eps,
+                                                rot, theta, true, tpt.data_as<int>(), tph.data_as<int>(),
+                                                tpw.data_as<int>(), P, dshift, sec_t, sec_h, sec_w);
+        u16v wq2(size_t(Hq) * D), wg2(size_t(Hq) * D), wk2 = dk;
+        orc_decode_prepare_rp(dq.data(), 1, wq2.data(), wg2.data(), wk2.data(), v.data(), qw.data(), kw.data(),
+                              nullptr, nullptr, 1, Hq, Hkv, D, 0, rot, theta, eps, &sp, 1, pt.data(), ph.data(),
+                              pw.data(), 0, P, dshift, nullptr, nullptr, sec_t, sec_h, sec_w);
+        u16v gk2 = download<uint16_t>(ctx, tdk), ck2 = download<uint16_t>(ctx, kc);
+        bool row_ok = true;
+        for (int h = 0; h < Hkv; ++h)
+          row_ok &= !std::memcmp(&ck2[(size_t(h) * max_seq + sp) * D], &gk2[size_t(h) * D], D * 2);
+        e = std::fmax(relerr(download<uint16_t>(ctx, qo2), wq2), relerr(gk2, wk2));
+        expect(e <= 1e-2 && row_ok && download<uint16_t>(ctx, go2) == wg2,
+               sp < P ? "decode_prepare_qgkv_packed_partial (mRoPE, in prompt)"
+                      : "decode_prepare_qgkv_packed_partial (text shift, cache row unshifted)",
+               e);
+      }
     }
-    expect(threw, "apply_rope_partial rejects interleaved mRoPE", 0);
   }
   // ---- whole DeltaNet layer: prefill over fused rows, then decode steps ----
   {

@@ -272,3 +272,131 @@ def test_apply_gate_needs_packed():
     import aila_amd
     with pytest.raises(ValueError):
         aila_amd.gqa_decode_prepare_append(None, None, None, None, None, 0, apply_gate=True)
+
+
+# ---- rotary positions past the cache row: text shift and interleaved mRoPE ----
+# (ElementwiseOps.cpp:33-103, 555-863; the oracle's position rule is pinned in
+# tests/test_oracle_mrope.py)
+
+def _streams(seed, B, P, hi=3000):
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, hi, (B, P)).astype(np.int32) for _ in range(3)]
+
+
+def _rope_pair(streams, plens, deltas, sec, per_seq=True):
+    """The same positions as a device record (aila_amd.rope_pos) and as the
+    oracle's dict."""
+    import aila_amd
+    st = streams if per_seq else [s[0] for s in streams]
+    dev = aila_amd.rope_pos(pos_t=_t(st[0]), pos_h=_t(st[1]), pos_w=_t(st[2]), sections=sec,
+                            prompt_pos_lens=_t(plens), text_pos_deltas=_t(deltas))
+    host = dict(pos_t=st[0], pos_h=st[1], pos_w=st[2], sections=sec, prompt_lens=plens, deltas=deltas)
+    return dev, host
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,rot,packed", [
+    (3, 16, 4, 256, 64, True),     # Qwen3.5 attention: partial rotary, packed q|gate
+    (3, 8, 2, 128, 128, False),
+])
+def test_decode_prepare_mrope(B, Hq, Hkv, D, rot, packed):
+    import torch
+    import aila_amd
+    seed, theta, eps, max_seq, P = 1700 + D, 1e7, 1e-6, 4096, 600
+    sec = (11, 11, 10) if rot == 64 else (24, 20, 20)
+    pos = np.array([300, 700, 4000], np.int32)
+    plens = np.array([P, 600, 0], np.int32)      # seq 0 inside its prompt, 1 and 2 past it
+    deltas = np.array([-100, -250, 9], np.int32)
+    dev, host = _rope_pair(_streams(seed, B, P), plens, deltas, sec)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D if packed else D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc_d = torch.zeros((B, Hkv, max_seq, D), dtype=torch.bfloat16, device="cuda")
+    vc_d = torch.zeros_like(kc_d)
+    k_d = _t(k)
+    res = aila_amd.decode_prepare_qkv(_t(q), k_d, _t(v), _t(qw), _t(kw), kc_d, vc_d, positions=_t(pos),
+                                      rotary_dim=rot, theta=theta, eps=eps, packed_gate=packed, rope=dev)
+    torch.cuda.synchronize()
+    q_got = res[0] if packed else res
+    qo, _, ko = oracle.decode_prepare(q, k, v, qw, kw, None, None, pos, B, Hq, Hkv, D, 0, rot, theta, eps,
+                                      packed=packed, rope=host)
+    _agree(_np(q_got), qo)
+    _agree(_np(k_d), ko)
+    # the rotation moved but the cache row did not
+    kc_h = _np(kc_d)
+    for b in range(B):
+        assert np.array_equal(kc_h[b, :, pos[b]], _np(k_d)[b])
+    assert int((kc_h != 0).any(axis=-1).sum()) == B * Hkv
+    # and it differs from a plain prep at the row (the positions matter)
+    plain = oracle.decode_prepare(q, k, v, qw, kw, None, None, pos, B, Hq, Hkv, D, 0, rot, theta, eps,
+                                  packed=packed)[0]
+    assert not np.array_equal(plain, qo)
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D,rot,start,P,delta", [
+    (80, 8, 2, 256, 64, 0, 50, -20),      # a prompt with image positions, then text
+    (33, 4, 4, 128, 128, 100, 120, 5),
+    (20, 2, 1, 64, 32, 500, 100, 1000),   # a later turn: every row past the prompt
+])
+def test_apply_rope_mrope(S, Hq, Hkv, D, rot, start, P, delta):
+    import torch
+    import aila_amd
+    sec = (rot // 6, rot // 6, rot // 2 - 2 * (rot // 6))
+    st = _streams(1800 + D, 1, P, hi=500)
+    q = dg.normal_bf16(1800 + D, 0, (S, Hq, D))
+    k = dg.normal_bf16(1800 + D, 1, (S, Hkv, D))
+    dev = aila_amd.rope_pos(prompt_pos_len=P, text_pos_delta=delta, pos_t=_t(st[0][0]), pos_h=_t(st[1][0]),
+                            pos_w=_t(st[2][0]), sections=sec)
+    qd, kd = _t(q), _t(k)
+    aila_amd.apply_rope(qd, kd, start_pos=start, rotary_dim=rot, theta=1e6, rope=dev)
+    torch.cuda.synchronize()
+    host = dict(pos_t=st[0][0], pos_h=st[1][0], pos_w=st[2][0], prompt_pos_len=P, text_pos_delta=delta,
+                sections=sec)
+    qw, kw = oracle.apply_rope(q.reshape(S, -1), k.reshape(S, -1), S, start, Hq, Hkv, D, rot, 1e6, rope=host)
+    _agree(_np(qd), qw.reshape(S, Hq, D))
+    _agree(_np(kd), kw.reshape(S, Hkv, D))
+    assert np.array_equal(_np(qd)[..., rot:], q[..., rot:])
+
+
+@pytest.mark.parametrize("apply_gate,split", [(True, True), (False, True), (True, False)])
+def test_fused_prepare_append_decode_mrope(apply_gate, split):
+    """The one-launch prep + append + decode with shifted / mRoPE positions
+    (the hybrid backend's decode after a multimodal prompt,
+    Qwen35HybridTextBackend.cpp:2109-2135) against the oracle's prep at those
+    positions followed by its attention over rows [0, pos]."""
+    import torch
+    import aila_amd
+    B, Hq, Hkv, D, rot, max_seq, P = 3, 16, 4, 256, 64, 2048, 900
+    seed, theta, eps = 1900, 1e7, 1e-6
+    sec = (11, 11, 10)
+    pos = np.array([400, 1200, 2047], np.int32)
+    plens = np.array([P, P, 0], np.int32)
+    deltas = np.array([-300, -600, 17], np.int32)
+    dev, host = _rope_pair(_streams(seed, B, P), plens, deltas, sec)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
+    kc_d, vc_d = _t(kc), _t(vc)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda") if split else None
+    res = aila_amd.gqa_decode_prepare_append(
+        _t(q), _t(k), _t(v), kc_d, vc_d, int(pos.max()), q_norm_w=_t(qw), k_norm_w=_t(kw), rotary_dim=rot,
+        theta=theta, eps=eps, packed_gate=True, apply_gate=apply_gate, positions=_t(pos), workspace=ws, rope=dev)
+    torch.cuda.synchronize()
+    out = res if apply_gate else res[0]
+    qo, gw, ko = oracle.decode_prepare(q, k, v, qw, kw, kc, vc, pos, B, Hq, Hkv, D, max_seq, rot, theta, eps,
+                                       packed=True, rope=host)
+    got = _np(out)
+    for b in range(B):
+        want = oracle.attention_decode_baseline(qo[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv, D, max_seq,
+                                                int(pos[b]) + 1)[0]
+        if apply_gate:
+            want = oracle.sigmoid_mul(want, gw[b])
+        assert _relerr(got[b], want) <= TOL, f"sequence {b}"
+    kc_h = _np(kc_d)
+    for b in range(B):
+        _agree(kc_h[b, :, pos[b]], ko[b])
