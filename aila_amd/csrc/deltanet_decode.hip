@@ -20,6 +20,7 @@
 // traffic. Measured with the state evicted from the caches (states used in
 // rotation): B = 32, H = 16: 13.9 -> 12.1 us; B = 8, Hv = 32: 10.1 -> 7.2 us.
 #include "common.hpp"
+#include "deltanet_generic.hpp"
 
 #include <type_traits>
 
@@ -183,11 +184,27 @@ extern "C" int aila_hip_deltanet_decode(const void* q, const void* k,
                                         void* stream) {
   using namespace aila;
   AILA_REQUIRE(q && k && v && a && b && state && out, "deltanet_decode: null pointer");
-  AILA_REQUIRE(B > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0,
-               "deltanet_decode: need B, Hk, Hv > 0 and Hv %% Hk == 0 (B=%d Hk=%d Hv=%d)", B, Hk, Hv);
-  AILA_REQUIRE(dv > 0 && dv % 4 == 0, "deltanet_decode: dv must be a positive multiple of 4 (dv=%d)", dv);
+  AILA_REQUIRE(B > 0 && Hk > 0 && Hv > 0 && dk > 0 && dv > 0,
+               "deltanet_decode: need B, Hk, Hv, dk, dv > 0 (B=%d Hk=%d Hv=%d dk=%d dv=%d)", B, Hk, Hv, dk, dv);
   AILA_REQUIRE(B <= 65535, "deltanet_decode: B too large (%d)", B);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (Hv % Hk != 0 || dv % 4 != 0 || (dk != 64 && dk != 128 && dk != 256)) {
+    // general shapes: one token of the sequential kernel
+    GenericDeltaNet g{};
+    g.q = static_cast<const bf16*>(q);
+    g.k = static_cast<const bf16*>(k);
+    g.v = static_cast<const bf16*>(v);
+    g.a = static_cast<const bf16*>(a);
+    g.b = static_cast<const bf16*>(b);
+    g.ab_stride = Hv;
+    g.dt_bias = static_cast<const bf16*>(dt_bias);
+    g.A_log = A_log;
+    g.state = state;
+    g.out = static_cast<bf16*>(out);
+    g.B = B, g.T = 1, g.Hk = Hk, g.Hv = Hv, g.dk = dk, g.dv = dv, g.K = 1;
+    g.eps = eps, g.scale = scale;
+    return deltanet_generic_launch(g, st, "deltanet_decode");
+  }
   const bf16* qp = static_cast<const bf16*>(q);
   const bf16* kp = static_cast<const bf16*>(k);
   const bf16* vp = static_cast<const bf16*>(v);

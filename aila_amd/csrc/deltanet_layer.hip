@@ -20,6 +20,7 @@
 // two reductions, as in the recurrence-only decode kernel: 1 read + 1 write
 // of the state per step.
 #include "common.hpp"
+#include "deltanet_generic.hpp"
 
 namespace aila {
 
@@ -434,7 +435,8 @@ size_t layer_ws_bytes(int B, int T, int Hv) { return deltanet_chunk_records_byte
 }  // namespace aila
 
 extern "C" size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk, int Hv, int dk, int dv) {
-  if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || dk != aila::kD || dv != aila::kD) return 0;
+  // 0 also for the shapes that run the sequential general-shape kernel
+  if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0 || dk != aila::kD || dv != aila::kD || Hv % Hk != 0) return 0;
   return aila::layer_ws_bytes(B, T, Hv);
 }
 
@@ -448,15 +450,38 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
   using namespace aila;
   AILA_REQUIRE(qkv && z && a && b && conv_w && conv_state && norm_w && state && out,
                "deltanet_layer_prefill: null pointer");
-  AILA_REQUIRE(dk == kD && dv == kD && conv_kernel == kConvK,
-               "deltanet_layer_prefill: needs dk = dv = 128 and conv kernel 4 (dk=%d dv=%d K=%d)", dk, dv,
+  AILA_REQUIRE(B > 0 && B <= 65535 && T > 0 && Hk > 0 && Hv > 0 && Hv <= 65535 && dk > 0 && dv > 0 &&
+                   conv_kernel >= 1,
+               "deltanet_layer_prefill: bad shape (B=%d T=%d Hk=%d Hv=%d dk=%d dv=%d K=%d)", B, T, Hk, Hv, dk, dv,
                conv_kernel);
-  AILA_REQUIRE(B > 0 && B <= 65535 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Hv <= 65535,
-               "deltanet_layer_prefill: bad shape (B=%d T=%d Hk=%d Hv=%d)", B, T, Hk, Hv);
-  const int qd = Hk * kD, vd = Hv * kD, ch = 2 * qd + vd;
+  const int qd = Hk * dk, vd = Hv * dv, ch = 2 * qd + vd;
   AILA_REQUIRE(qkv_stride >= ch && z_stride >= vd && ab_stride >= Hv,
                "deltanet_layer_prefill: row strides too small (qkv %d < %d, z %d, ab %d)", qkv_stride, ch, z_stride,
                ab_stride);
+  if (!(dk == kD && dv == kD && conv_kernel == kConvK && Hv % Hk == 0)) {
+    // general shapes: the token-sequential layer kernel (no workspace)
+    GenericDeltaNet g{};
+    g.layer = 1;
+    g.qkv = static_cast<const bf16*>(qkv);
+    g.qkv_stride = qkv_stride;
+    g.z = static_cast<const bf16*>(z);
+    g.z_stride = z_stride;
+    g.conv_w = static_cast<const bf16*>(conv_w);
+    g.conv_state = conv_state;
+    g.conv_head = conv_head;
+    g.K = conv_kernel;
+    g.norm_w = norm_w;
+    g.a = static_cast<const bf16*>(a);
+    g.b = static_cast<const bf16*>(b);
+    g.ab_stride = ab_stride;
+    g.dt_bias = static_cast<const bf16*>(dt_bias);
+    g.A_log = A_log;
+    g.state = state;
+    g.out = static_cast<bf16*>(out);
+    g.B = B, g.T = T, g.Hk = Hk, g.Hv = Hv, g.dk = dk, g.dv = dv;
+    g.eps = eps, g.scale = scale;
+    return deltanet_generic_launch(g, static_cast<hipStream_t>(stream), "deltanet_layer_prefill");
+  }
   AILA_REQUIRE(aligned(qkv, 8) && qkv_stride % 4 == 0 && aligned(conv_w, 16) && aligned(conv_state, 16) &&
                    aligned(z, 16) && z_stride % 8 == 0 && aligned(norm_w, 16) && aligned(state, 16) &&
                    aligned(out, 16),
@@ -494,15 +519,40 @@ extern "C" int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride, c
   using namespace aila;
   AILA_REQUIRE(qkv && z && a && b && conv_w && conv_state && norm_w && state && out,
                "deltanet_layer_decode: null pointer");
-  AILA_REQUIRE(dk == kD && dv == kD && conv_kernel == kConvK,
-               "deltanet_layer_decode: needs dk = dv = 128 and conv kernel 4 (dk=%d dv=%d K=%d)", dk, dv,
+  AILA_REQUIRE(B > 0 && B <= 65535 && Hk > 0 && Hv > 0 && dk > 0 && dv > 0 && conv_kernel >= 1,
+               "deltanet_layer_decode: bad shape (B=%d Hk=%d Hv=%d dk=%d dv=%d K=%d)", B, Hk, Hv, dk, dv,
                conv_kernel);
-  AILA_REQUIRE(B > 0 && B <= 65535 && Hk > 0 && Hv > 0 && Hv % Hk == 0,
-               "deltanet_layer_decode: bad B/Hk/Hv (B=%d Hk=%d Hv=%d)", B, Hk, Hv);
   const int ch = 2 * Hk * dk + Hv * dv;
   AILA_REQUIRE(qkv_stride >= ch && z_stride >= Hv * dv && ab_stride >= Hv,
                "deltanet_layer_decode: row strides too small (qkv %d < %d, z %d, ab %d)", qkv_stride, ch,
                z_stride, ab_stride);
+  if (!(dk == kD && dv == kD && conv_kernel == kConvK && Hv % Hk == 0 &&
+        (Hv / Hk == 1 || Hv / Hk == 2 || Hv / Hk == 4))) {
+    // general shapes: one token of the sequential layer kernel, then the
+    // ring rewrite
+    GenericDeltaNet g{};
+    g.layer = 1;
+    g.qkv = static_cast<const bf16*>(qkv);
+    g.qkv_stride = qkv_stride;
+    g.z = static_cast<const bf16*>(z);
+    g.z_stride = z_stride;
+    g.conv_w = static_cast<const bf16*>(conv_w);
+    g.conv_state = conv_state;
+    g.conv_head = conv_head;
+    g.conv_heads = conv_heads;
+    g.K = conv_kernel;
+    g.norm_w = norm_w;
+    g.a = static_cast<const bf16*>(a);
+    g.b = static_cast<const bf16*>(b);
+    g.ab_stride = ab_stride;
+    g.dt_bias = static_cast<const bf16*>(dt_bias);
+    g.A_log = A_log;
+    g.state = state;
+    g.out = static_cast<bf16*>(out);
+    g.B = B, g.T = 1, g.Hk = Hk, g.Hv = Hv, g.dk = dk, g.dv = dv;
+    g.eps = eps, g.scale = scale;
+    return deltanet_generic_launch(g, static_cast<hipStream_t>(stream), "deltanet_layer_decode");
+  }
   AILA_REQUIRE(aligned(conv_w, 8) && aligned(z, 8) && z_stride % 4 == 0 && aligned(norm_w, 16) &&
                    aligned(state, 16) && aligned(out, 8) && aligned(arrivals, 4),
                "deltanet_layer_decode: misaligned conv_w/z/norm_w/state/out/arrivals");

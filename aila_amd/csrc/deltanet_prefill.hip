@@ -49,6 +49,7 @@
 // group g (= lane / 16) supplies k = {4g..4g+3, 16+4g..16+4g+3}. The
 // workspace stores W (over k), K^T and P (over tokens) in that order.
 #include "common.hpp"
+#include "deltanet_generic.hpp"
 
 #include <type_traits>
 
@@ -971,6 +972,7 @@ void launch_deltanet_chunked(const bf16* q, const bf16* k, const bf16* v, const 
 }  // namespace aila
 
 extern "C" size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk, int dv) {
+  // 0 also for the shapes that run the sequential general-shape kernel
   if (B <= 0 || T <= 0 || Hv <= 0 || dk != 128 || dv != 128) return 0;
   return aila::deltanet_chunk_records_bytes(B, T, Hv, false);
 }
@@ -982,10 +984,25 @@ extern "C" int aila_hip_deltanet_prefill(const void* q, const void* k, const voi
                                          int dk, int dv, float eps, float scale, void* stream) {
   using namespace aila;
   AILA_REQUIRE(q && k && v && a && b && state && out, "deltanet_prefill: null pointer");
-  AILA_REQUIRE(B > 0 && B <= 65535 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Hv <= 65535,
+  AILA_REQUIRE(B > 0 && B <= 65535 && T > 0 && Hk > 0 && Hv > 0 && Hv <= 65535,
                "deltanet_prefill: bad shape (B=%d T=%d Hk=%d Hv=%d)", B, T, Hk, Hv);
-  if (dk != 128 || dv != 128)
-    return set_error(AILA_HIP_EUNSUPPORTED, "deltanet_prefill: dk=%d dv=%d (only 128/128)", dk, dv);
+  if (dk != 128 || dv != 128 || Hv % Hk != 0) {
+    // general shapes: the token-sequential kernel (no workspace)
+    GenericDeltaNet g{};
+    g.q = static_cast<const bf16*>(q);
+    g.k = static_cast<const bf16*>(k);
+    g.v = static_cast<const bf16*>(v);
+    g.a = static_cast<const bf16*>(a);
+    g.b = static_cast<const bf16*>(b);
+    g.ab_stride = Hv;
+    g.dt_bias = static_cast<const bf16*>(dt_bias);
+    g.A_log = A_log;
+    g.state = state;
+    g.out = static_cast<bf16*>(out);
+    g.B = B, g.T = T, g.Hk = Hk, g.Hv = Hv, g.dk = dk, g.dv = dv, g.K = 1;
+    g.eps = eps, g.scale = scale;
+    return deltanet_generic_launch(g, static_cast<hipStream_t>(stream), "deltanet_prefill");
+  }
   const size_t need = aila_hip_deltanet_prefill_workspace_size(B, T, Hv, dk, dv);
   if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_prefill: workspace %zu < %zu bytes", workspace_bytes, need);

@@ -270,8 +270,12 @@ int aila_hip_copy_to_cache(const void* new_kv, void* cache, int S,
  *   state [B, Hv, dk, dv] fp32, S[j*dv + i], updated in place:
  *     S *= decay; u = S^T k; d = (v - u) * beta; S += k d^T
  *   out  [B, Hv, dv] bf16 = (S^T q) * scale.
- * Value head hv uses key head hv / (Hv / Hk). The state is read once and
- * written once. Supported: dk in {64, 128, 256}, dv a multiple of 4. */
+ * Value head hv uses key head hv / (Hv / Hk) (clamp(hv, 0, Hk - 1) when Hk
+ * does not divide Hv, as Qwen35HybridTextBackend.cpp:104-118). The state is
+ * read once and written once. Tuned kernels: dk in {64, 128, 256}, dv a
+ * multiple of 4, Hk dividing Hv; other shapes with dk, dv <= 256 run a
+ * general-shape kernel (one workgroup per value head and sequence, state
+ * in global memory, same math). */
 int aila_hip_deltanet_decode(const void* q, const void* k, const void* v,
                              const void* a, const void* b,
                              const void* dt_bias, const float* A_log,
@@ -294,9 +298,13 @@ int aila_hip_deltanet_decode(const void* q, const void* k, const void* v,
  *         the fused row width for the backend's [qkv | z | a | b] row).
  *   gate: out[b, hv, :] = bf16(rmsnorm(o) * norm_w * silu(z)), rmsnorm over dv,
  *         z row b at z + b*z_stride, norm_w [dv] fp32 (:1153-1160, :153-173).
- * state [B, Hv, dk, dv] fp32 is read and written once. Supported: dk = dv =
- * 128, conv kernel 4, Hv / Hk in {1, 2, 4} (the reference fast path's
- * shapes).
+ * state [B, Hv, dk, dv] fp32 is read and written once. Tuned kernels: dk =
+ * dv = 128, conv kernel 4, Hv / Hk in {1, 2, 4} (the reference fast path's
+ * shapes). Other shapes (dk, dv <= 256, conv kernel 1..16, any head counts,
+ * key head as aila_hip_deltanet_decode) run the general-shape kernel, the
+ * role of the reference's generic fallback (:1168-1304), followed by a
+ * ring-rewrite launch; conv_state is then [B, K-1, ch] and arrivals is
+ * ignored.
  *   arrivals  optional device uint32[B*Hk], zero before the first call and
  *             left zero by every call: with it (and Hv > Hk) the layer runs
  *             one workgroup per value head instead of one per key head (the
@@ -318,8 +326,8 @@ int aila_hip_deltanet_layer_decode(const void* qkv, int qkv_stride,
 
 /* Workspace bytes for aila_hip_deltanet_layer_prefill: the per-chunk
  * records (as aila_hip_deltanet_prefill's, plus the key residual; about
- * 121 KiB per sequence, value head and 64-token chunk). 0 for unsupported
- * shapes. */
+ * 121 KiB per sequence, value head and 64-token chunk). 0 for the shapes
+ * that run the general-shape kernel (no workspace needed). */
 size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
                                                       int Hv, int dk, int dv);
 
@@ -336,9 +344,11 @@ size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
  * + SiLU of its rows itself and carries it fp32-accurate (bf16 hi +
  * residual) into the recurrence, which runs chunked as
  * aila_hip_deltanet_prefill; the last pass applies the gated RMSNorm and
- * rewrites the ring. out [B, T, Hv*dv] bf16. Supported: dk = dv = 128,
+ * rewrites the ring. out [B, T, Hv*dv] bf16. Chunked path: dk = dv = 128,
  * conv kernel 4, Hv % Hk == 0; qkv 8-byte aligned with qkv_stride a
- * multiple of 4 and T*qkv_stride*2 < 2^31. */
+ * multiple of 4 and T*qkv_stride*2 < 2^31. Other shapes (dk, dv <= 256,
+ * conv kernel 1..16, any head counts) run the general-shape kernel token by
+ * token, as the reference's batched prefill does; no workspace. */
 int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,
                                     const void* z, int z_stride, const void* a,
                                     const void* b, int ab_stride,
@@ -353,8 +363,8 @@ int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,
 
 /* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W and its
  * residual, U, P, Q, K^T and decay factors, in the scan's operand order;
- * 105 KiB per (sequence, value head, 64-token chunk)). 0 for unsupported
- * shapes. */
+ * 105 KiB per (sequence, value head, 64-token chunk)). 0 for the shapes that
+ * run the general-shape kernel. */
 size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk,
                                                 int dv);
 
@@ -366,7 +376,8 @@ size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk,
  *   dt_bias [Hv] bf16 / A_log [Hv] fp32 may be NULL
  *   state [B, Hv, dk, dv] fp32: initial state in, final state out
  *   out [B, T, Hv, dv] bf16
- * Supported: dk = dv = 128. */
+ * Chunked path: dk = dv = 128 with Hk dividing Hv; other shapes (dk, dv <=
+ * 256) run the general-shape kernel token by token (no workspace). */
 int aila_hip_deltanet_prefill(const void* q, const void* k, const void* v,
                               const void* a, const void* b,
                               const void* dt_bias, const float* A_log,
