@@ -46,6 +46,10 @@ def test_argument_validation_runs_before_any_device_work():
     ws = ctypes.c_void_p(4096)
     rc = l.aila_hip_gqa_decode(p, p, p, p, ws, 100, 1, 16, 8, 128, 512, 10, None, None)
     assert rc == -4   # workspace too small for two split records
-    rc = l.aila_hip_deltanet_decode(p, p, p, p, p, None, None, p, p, 1, 3, 4, 128, 128,
+    rc = l.aila_hip_deltanet_decode(p, p, p, p, p, None, None, p, p, 1, 3, 4, 0, 128,
                                     1e-6, 0.1, None)
-    assert rc == -1 and b"Hv % Hk" in l.aila_hip_last_error()
+    assert rc == -1 and b"dk" in l.aila_hip_last_error()
+    # head dims beyond every kernel (the general-shape one stops at 256)
+    rc = l.aila_hip_deltanet_decode(p, p, p, p, p, None, None, p, p, 1, 3, 4, 320, 128,
+                                    1e-6, 0.1, None)
+    assert rc == -2 and b"dk=320" in l.aila_hip_last_error()
