@@ -27,6 +27,7 @@ _SIGS = {
     "aila_hip_version": ([], _I),
     "aila_hip_gqa_decode_workspace_size": ([_I, _I, _I], _SZ),
     "aila_hip_gqa_decode": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "aila_hip_gqa_decode_window": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P], _I),
     "aila_hip_gqa_decode_paged": ([_P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P], _I),
     "aila_hip_kv_append_paged": ([_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P], _I),
     "aila_hip_gqa_decode_noalloc_max_bytes": ([], _SZ),
@@ -171,12 +172,14 @@ def gqa_decode_workspace_size(B: int, Hq: int, D: int) -> int:
 
 
 def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
-               seq_lens=None, stream=None):
+               seq_lens=None, window=None, stream=None):
     """q [B,Hq,D] bf16; k_cache/v_cache [B,Hkv,max_seq,D] bf16 -> out [B,Hq,D].
 
     ``workspace``: uint8 device tensor of >= gqa_decode_workspace_size bytes
     enables split-K; None runs the single-pass kernel. ``seq_lens``: optional
-    int32 [B] device tensor of per-sequence lengths (<= cached_len)."""
+    int32 [B] device tensor of per-sequence lengths (<= cached_len).
+    ``window``: optional (window, window_start, sink) — the reference's
+    decode window with attention sinks (window_start -1: max(512, window))."""
     import torch
     B, Hq, D = q.shape
     Hkv, max_seq = k_cache.shape[1], k_cache.shape[2]
@@ -193,6 +196,13 @@ def gqa_decode(q, k_cache, v_cache, cached_len: int, out=None, workspace=None,
         ws_bytes = workspace.numel() * workspace.element_size()
     if seq_lens is not None:
         _need(seq_lens, torch.int32, (B,), "seq_lens", align=4)
+    if window is not None:
+        w, ws0, sink = (int(x) for x in window)
+        rc = lib().aila_hip_gqa_decode_window(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
+                                              _ptr(workspace), ws_bytes, B, Hq, Hkv, D, max_seq,
+                                              int(cached_len), _ptr(seq_lens), w, ws0, sink, _stream(stream))
+        _check(rc, "aila_hip_gqa_decode_window")
+        return out
     rc = lib().aila_hip_gqa_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out),
                                    _ptr(workspace), ws_bytes, B, Hq, Hkv, D, max_seq,
                                    int(cached_len), _ptr(seq_lens), _stream(stream))

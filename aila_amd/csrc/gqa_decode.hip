@@ -76,6 +76,34 @@ struct PageArgs {
   int max_pages;
 };
 
+// Decode window with attention sinks (ops::attention_decode's
+// AILA_ATTN_DECODE_WINDOW / _WINDOW_START / _SINK knobs,
+// AttentionOps.cpp:533-551, 598-616): once a sequence holds more than
+// `start` rows it attends its first `sink` rows and its last `window` rows
+// only. window = 0: off.
+struct WinArgs {
+  int window, start, sink;
+};
+// The attended rows of a sequence of L cached rows as a logical range
+// [0, len): logical row t is cache row t below `sink` and t + gap above.
+struct WinPlan {
+  int len, sink, gap;
+};
+__host__ __device__ __forceinline__ WinPlan window_plan(int L, const WinArgs& w) {
+  const bool apply = w.window > 0 && L > w.start;
+  const int eff_window = apply ? (L < w.window ? L : w.window) : L;
+  int tail = L - eff_window;
+  int sink = 0;
+  if (apply && w.sink > 0) sink = w.sink < tail ? w.sink : tail;
+  int len = eff_window + sink;
+  if (len >= L) {   // sink and tail meet: the whole context (AttentionOps.cpp:612-616)
+    tail = 0;
+    sink = 0;
+    len = L;
+  }
+  return WinPlan{len, sink, tail - sink};
+}
+
 // Rows per split of one sequence. With a host length the host plan's
 // split_len holds. With device lengths the launch is sized for a bound (the
 // capacity a captured graph replays with), so the launched nsplit splits
@@ -88,15 +116,17 @@ __device__ __forceinline__ int split_rows(int len, int split_len, int nsplit, bo
   return max(kChunk, (per + kChunk - 1) / kChunk * kChunk);
 }
 
-template <int D, int G, bool PREP = false, bool PAGED = false>
+template <int D, int G, bool PREP = false, bool PAGED = false, bool WIN = false>
 __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kc,
     const bf16* __restrict__ vc, bf16* __restrict__ out,
     float* __restrict__ part, int Hq, int Hkv, int max_seq, int L,
     const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max,
-    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new, PrepArgs pa, PageArgs pg) {
+    float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new, PrepArgs pa, PageArgs pg,
+    WinArgs wn) {
   static_assert(D % 32 == 0 && D <= 256, "D");
   static_assert(!(PAGED && PREP), "the paged variant has no fused preparation");
+  static_assert(!(WIN && (PAGED || PREP)), "the window variant is contiguous and has no fused append");
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "G");
   constexpr int KS = D / 32;          // MFMA k-steps over the head dim
   constexpr int VL = D / 8;           // lanes per V row (16 B each)
@@ -109,6 +139,16 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   int len = L;
   if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
+  // window: logical row t reads cache row t (t < wsink) or t + wgap
+  int wsink = 0, wgap = 0;
+  if constexpr (WIN) {
+    const WinPlan wp = window_plan(len, wn);
+    len = wp.len;
+    wsink = wp.sink;
+    wgap = wp.gap;
+  } else {
+    (void)wn;
+  }
   const int sl = split_rows(len, split_len, static_cast<int>(gridDim.x), seq_lens != nullptr);
   const int s0 = split * sl;
   const int nsplit_b = (len + sl - 1) / sl;
@@ -176,8 +216,14 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
       const int p = i * 64 + lane;
       const int r = p / NC, qc = (p % NC) ^ kswz<D>(r);
       const int tok = min(t0 + r, s1 - 1) - t0;
-      __builtin_amdgcn_global_load_lds(Kc + static_cast<size_t>(tok) * D + qc * 8,
-                                       (lds_void_t*)(dst + i * 1024), 16, 0, kNontemporal);
+      const bf16* src;
+      if constexpr (WIN) {
+        const int t = t0 + tok;
+        src = K + static_cast<size_t>(t < wsink ? t : t + wgap) * D + qc * 8;
+      } else {
+        src = Kc + static_cast<size_t>(tok) * D + qc * 8;
+      }
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst + i * 1024), 16, 0, kNontemporal);
     }
   };
 
@@ -341,7 +387,14 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 #pragma unroll
     for (int i = 0; i < kChunk / VR; ++i) {
       const int tok = min(t0 + vr + i * VR, s1 - 1) - t0;
-      vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Vc + static_cast<size_t>(tok) * D + vd));
+      const bf16* src;
+      if constexpr (WIN) {
+        const int t = t0 + tok;
+        src = V + static_cast<size_t>(t < wsink ? t : t + wgap) * D + vd;
+      } else {
+        src = Vc + static_cast<size_t>(tok) * D + vd;
+      }
+      vv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
     }
     const int t_next = t0 + kWaves * kChunk;
     if (t_next < s1) dma_k(stage ^ 1, t_next, pg_nxt);
@@ -490,16 +543,18 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 // Thread t owns 4 head dims (float4 column c) of the splits i = part (mod P),
 // so its record reads are independent and issued together; the P partial
 // sums meet in LDS.
-template <int D>
+template <int D, bool WIN = false>
 __global__ __launch_bounds__(256) void gqa_decode_merge_kernel(
     const float* __restrict__ part, bf16* __restrict__ out, int Hq, int L,
     const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit, int nsplit_max,
-    const bf16* __restrict__ gate, int gate_stride) {
+    const bf16* __restrict__ gate, int gate_stride, WinArgs wn) {
   constexpr int C4 = D / 4;             // float4 columns
   constexpr int P = 256 / C4;           // split phases
   const int hq = blockIdx.x, b = blockIdx.y;
   int len = L;
   if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
+  if constexpr (WIN) len = window_plan(len, wn).len;
+  else (void)wn;
   const int sl = split_rows(len, split_len, nsplit, seq_lens != nullptr);
   const int ns = (len + sl - 1) / sl;
   const float* rec0 = part + (static_cast<size_t>(b) * Hq + hq) * nsplit_max * (kRecHeader + D);
@@ -596,28 +651,39 @@ struct DecodeArgs {
   const bf16* v_new;
   PrepArgs prep;         // q_stride = 0: no fused preparation
   PageArgs pages;        // table = null: contiguous [B, Hkv, max_seq, D] cache
+  WinArgs win;           // window = 0: every row
 };
 
 template <int D, int G>
 int launch_decode(const DecodeArgs& a, hipStream_t st) {
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+  const bool win = a.win.window > 0;
   if (a.prep.q_stride > 0)
     hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
   else if (a.pages.table != nullptr)
     hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0,
                        st, a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
+  else if (win)
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, false, true>), dim3(a.nsplit, a.Hkv, a.B),
+                       dim3(kThreads), 0, st, a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L,
+                       a.seq_lens, a.len_bias, a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep,
+                       a.pages, a.win);
   else
     hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages);
+                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
   if (a.part) {
     const bool gated = a.prep.q_stride > 0 && a.prep.apply_gate;
-    hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
-                       a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit, a.nsplit_max,
-                       gated ? a.q + D : nullptr, a.prep.q_stride);
+    if (win)
+      hipLaunchKernelGGL((gqa_decode_merge_kernel<D, true>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
+                         a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit, a.nsplit_max, nullptr, 0, a.win);
+    else
+      hipLaunchKernelGGL((gqa_decode_merge_kernel<D>), dim3(a.Hq, a.B), dim3(256), 0, st, a.part, a.out, a.Hq,
+                         a.L, a.seq_lens, a.len_bias, a.split_len, a.nsplit, a.nsplit_max,
+                         gated ? a.q + D : nullptr, a.prep.q_stride, a.win);
   }
   return check_launch("gqa_decode");
 }
@@ -679,7 +745,8 @@ int dispatch_g(int G, const DecodeArgs& a, hipStream_t st) {
 int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, void* out, void* workspace,
                     size_t workspace_bytes, int B, int Hq, int Hkv, int D, int max_seq, int cached_len,
                     const int* seq_lens, int len_bias, const void* k_new, const void* v_new,
-                    hipStream_t st, const PrepArgs* prep = nullptr, const PageArgs* pages = nullptr) {
+                    hipStream_t st, const PrepArgs* prep = nullptr, const PageArgs* pages = nullptr,
+                    const WinArgs* win = nullptr) {
   AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
   AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
                "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
@@ -696,6 +763,10 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
   a.v_new = static_cast<const bf16*>(v_new);
   a.prep = prep ? *prep : PrepArgs{};
   a.pages = pages ? *pages : PageArgs{};
+  a.win = win ? *win : WinArgs{};
+  // the split plan covers the rows a sequence of the bound length attends
+  // (the window's attended count never decreases with the length)
+  const int plan_len = a.win.window > 0 ? window_plan(cached_len, a.win).len : cached_len;
   // Records per (sequence, head) that the workspace holds; the split count
   // adapts to it (the reference's [Hq, max_tiles, 272] partials buffer for
   // D=256 is accepted as-is).
@@ -704,7 +775,7 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
   if (workspace && a.nsplit_max < 2)
     return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu bytes holds < 2 split records (%zu bytes each)",
                      workspace_bytes, rec_bytes);
-  if (cached_len == 0) {
+  if (plan_len == 0) {
     // Nothing to attend: the single-pass kernel writes a zero output.
     a.split_len = 1;
     a.nsplit = 1;
@@ -717,12 +788,12 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
     const int resident = resident_for(D, Hq / Hkv);
     int want = (resident + groups - 1) / groups;
     want = std::max(1, std::min(want, a.nsplit_max));
-    a.split_len = (cached_len + want - 1) / want;
+    a.split_len = (plan_len + want - 1) / want;
     a.split_len = ((a.split_len + kWaves * kChunk - 1) / (kWaves * kChunk)) * (kWaves * kChunk);
-    a.nsplit = (cached_len + a.split_len - 1) / a.split_len;
+    a.nsplit = (plan_len + a.split_len - 1) / a.split_len;
     if (a.nsplit > 1) a.part = static_cast<float*>(workspace);   // one split: direct output
   } else {
-    a.split_len = cached_len;
+    a.split_len = plan_len;
     a.nsplit = 1;
   }
   switch (D) {
@@ -746,6 +817,17 @@ extern "C" int aila_hip_gqa_decode(const void* q, const void* k_cache, const voi
                                    int max_seq, int cached_len, const int* seq_lens, void* stream) {
   return aila::gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq,
                                cached_len, seq_lens, 0, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aila_hip_gqa_decode_window(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                          void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int D,
+                                          int max_seq, int cached_len, const int* seq_lens, int window,
+                                          int window_start, int sink, void* stream) {
+  using namespace aila;
+  AILA_REQUIRE(window >= 0, "gqa_decode_window: window=%d < 0", window);
+  WinArgs w{window, window_start < 0 ? std::max(512, window) : window_start, std::max(0, sink)};
+  return gqa_decode_impl(q, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, cached_len,
+                         seq_lens, 0, nullptr, nullptr, static_cast<hipStream_t>(stream), nullptr, nullptr, &w);
 }
 
 extern "C" int aila_hip_gqa_decode_paged(const void* q, const void* k_pages, const void* v_pages, void* out,

@@ -26,10 +26,19 @@ void copy_to_cache(Context& ctx, Tensor& new_kv, Tensor& cache, int seq_len, int
 // does at AttentionOps.cpp:87); output [1, Hq*D]. scores_buf is accepted and
 // unused. exact_partials_buf (fp32, e.g. the backend's [Hq, max_tiles, 272]
 // buffer) enables split-K with as many splits as it holds records; null runs
-// the single-pass kernel.
+// the single-pass kernel. Like the reference it reads the decode window
+// knobs AILA_ATTN_DECODE_WINDOW / _WINDOW_START / _SINK once
+// (AttentionOps.cpp:517-551; window 0, the default, attends every row).
 void attention_decode(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output,
                       Tensor& scores_buf, int num_heads, int num_kv_heads, int head_dim,
                       int cached_len, Tensor* exact_partials_buf = nullptr);
+
+// The same with the window knobs as arguments: a sequence of more than
+// window_start rows (< 0: max(512, window)) attends its first `sink` and last
+// `window` rows only (AttentionOps.cpp:598-616).
+void attention_decode_window(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output,
+                             Tensor& scores_buf, int num_heads, int num_kv_heads, int head_dim, int cached_len,
+                             Tensor* exact_partials_buf, int window, int window_start, int sink);
 
 // The same decode over a paged KV cache (an addition behind the same shim;
 // the reference keeps one contiguous cache per sequence): k_pages/v_pages

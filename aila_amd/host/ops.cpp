@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <stdexcept>
 #include <string>
 
@@ -32,9 +33,30 @@ void copy_to_cache(Context& ctx, Tensor& new_kv, Tensor& cache, int seq_len, int
         "copy_to_cache");
 }
 
+namespace {
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  if (v == nullptr || *v == '\0') return dflt;
+  char* end = nullptr;
+  const long x = std::strtol(v, &end, 10);
+  return end && *end == '\0' ? static_cast<int>(x) : dflt;
+}
+}  // namespace
+
 void attention_decode(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output,
                       Tensor& scores_buf, int num_heads, int num_kv_heads, int head_dim,
                       int cached_len, Tensor* exact_partials_buf) {
+  // The reference's decode window knobs, read once (AttentionOps.cpp:517-551).
+  static const int window = std::max(0, env_int("AILA_ATTN_DECODE_WINDOW", 0));
+  static const int window_start = env_int("AILA_ATTN_DECODE_WINDOW_START", -1);
+  static const int sink = std::max(0, env_int("AILA_ATTN_DECODE_SINK", 0));
+  attention_decode_window(ctx, q, k_cache, v_cache, output, scores_buf, num_heads, num_kv_heads, head_dim,
+                          cached_len, exact_partials_buf, window, window_start, sink);
+}
+
+void attention_decode_window(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output,
+                             Tensor& scores_buf, int num_heads, int num_kv_heads, int head_dim, int cached_len,
+                             Tensor* exact_partials_buf, int window, int window_start, int sink) {
   (void)scores_buf;
   need_dtype(q, DType::bf16, "attention_decode q");
   need_dtype(k_cache, DType::bf16, "attention_decode k_cache");
@@ -52,10 +74,16 @@ void attention_decode(Context& ctx, Tensor& q, Tensor& k_cache, Tensor& v_cache,
       ws_bytes = 0;
     }
   }
-  check(aila_hip_gqa_decode(q.data(), k_cache.data(), v_cache.data(), output.data(), ws, ws_bytes, 1,
-                            num_heads, num_kv_heads, head_dim, max_seq, cached_len, nullptr,
-                            ctx.stream()),
-        "attention_decode");
+  if (window > 0)
+    check(aila_hip_gqa_decode_window(q.data(), k_cache.data(), v_cache.data(), output.data(), ws, ws_bytes, 1,
+                                     num_heads, num_kv_heads, head_dim, max_seq, cached_len, nullptr, window,
+                                     window_start, sink, ctx.stream()),
+          "attention_decode");
+  else
+    check(aila_hip_gqa_decode(q.data(), k_cache.data(), v_cache.data(), output.data(), ws, ws_bytes, 1,
+                              num_heads, num_kv_heads, head_dim, max_seq, cached_len, nullptr,
+                              ctx.stream()),
+          "attention_decode");
 }
 
 void attention_decode_paged(Context& ctx, Tensor& q, Tensor& k_pages, Tensor& v_pages, Tensor& block_table,

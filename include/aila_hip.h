@@ -97,6 +97,22 @@ int aila_hip_gqa_decode(const void* q, const void* k_cache, const void* v_cache,
                         int B, int Hq, int Hkv, int D, int max_seq,
                         int cached_len, const int* seq_lens, void* stream);
 
+/* The same decode over a window of each sequence's cache with attention
+ * sinks: the AILA_ATTN_DECODE_WINDOW / _WINDOW_START / _SINK knobs of
+ * ops::attention_decode (src/ops/AttentionOps.cpp:533-551, 598-616, and the
+ * tail_start / sink_len row map of :73-166, 168-320). A sequence of L rows
+ * with L > window_start attends rows [0, s) and [L - w, L), where
+ * w = min(L, window) and s = min(sink, L - w); when s + w >= L, or window = 0,
+ * or L <= window_start, it attends all L rows. window_start < 0 means
+ * max(512, window), the reference's default. L is cached_len, or
+ * min(seq_lens[b], cached_len) per sequence. Other arguments and results as
+ * aila_hip_gqa_decode; rows outside the window are never read. */
+int aila_hip_gqa_decode_window(const void* q, const void* k_cache, const void* v_cache,
+                               void* out, void* workspace, size_t workspace_bytes,
+                               int B, int Hq, int Hkv, int D, int max_seq,
+                               int cached_len, const int* seq_lens, int window,
+                               int window_start, int sink, void* stream);
+
 /* GQA decode over a paged KV cache. The reference keeps one contiguous
  * [Hkv, max_seq, D] cache per sequence (src/memory/KVCache.hpp:9-45) and
  * has no paged layout; this is the paged option of the same decode

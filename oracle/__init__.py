@@ -29,6 +29,7 @@ _SIGS = {
     "orc_num_threads": [],
     "orc_set_num_threads": [_I],
     "orc_attention_decode_baseline": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
+    "orc_attention_decode_window": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I],
     "orc_attention_decode_splitk": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "orc_attention_prefill_naive": [_P, _P, _P, _P, _I, _I, _I, _I],
     "orc_attention_prefill_online": [_P, _P, _P, _P, _I, _I, _I, _I, _I],
@@ -94,6 +95,17 @@ def attention_decode_baseline(q, kc, vc, B, Hq, Hkv, D, max_seq, L, fast=False):
     q, kc, vc = _c(q, U16), _c(kc, U16), _c(vc, U16)
     out = np.zeros((B, Hq, D), U16)
     lib(fast).orc_attention_decode_baseline(_p(q), _p(kc), _p(vc), _p(out), B, Hq, Hkv, D, max_seq, L)
+    return out
+
+
+def attention_decode_window(q, kc, vc, B, Hq, Hkv, D, max_seq, L, window, window_start, sink, lens=None):
+    """ops::attention_decode with the decode window / sink knobs; per-sequence
+    lengths ``lens`` (int [B]) or L for all."""
+    q, kc, vc = _c(q, U16), _c(kc, U16), _c(vc, U16)
+    lens = None if lens is None else np.ascontiguousarray(lens, dtype=np.int32)
+    out = np.zeros((B, Hq, D), U16)
+    lib().orc_attention_decode_window(_p(q), _p(kc), _p(vc), _p(out), B, Hq, Hkv, D, max_seq, L, _p(lens),
+                                      int(window), int(window_start), int(sink))
     return out
 
 

@@ -72,12 +72,15 @@ void orc_set_num_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 static inline float bf(bf16_t h) { return orc_bf16_to_f32(h); }
 
 // ------------------------------------------------------ GQA decode --------
-// attention_decode_baseline, AttentionOps.cpp:73-166 (contiguous mode:
-// sink_len = 0, tail_start = 0, effective_len = cached_len, :611-616).
+// attention_decode_baseline, AttentionOps.cpp:73-166: the effective_len
+// attended rows map to cache rows t (t < sink_len) and
+// tail_start + (t - sink_len) (:109, :160). Contiguous mode is sink_len = 0,
+// tail_start = 0, effective_len = cached_len (:611-616).
 // One sequence: q/out [Hq, D], cache [Hkv, max_seq, D].
-static void decode_baseline_one(const bf16_t* q, const bf16_t* kc,
-                                const bf16_t* vc, bf16_t* out, int Hq,
-                                int Hkv, int D, int max_seq, int L) {
+static void decode_baseline_rows(const bf16_t* q, const bf16_t* kc,
+                                 const bf16_t* vc, bf16_t* out, int Hq,
+                                 int Hkv, int D, int max_seq, int tail_start,
+                                 int sink_len, int L) {
   const int heads_per_kv = Hq / Hkv;                     // :85
   const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // :86
 #pragma omp parallel for schedule(static)
@@ -86,7 +89,8 @@ static void decode_baseline_one(const bf16_t* q, const bf16_t* kc,
     std::vector<float> qf(D), sc(L > 0 ? L : 1);
     for (int d = 0; d < D; ++d) qf[d] = bf(q[h * D + d]);        // :102-104
     for (int t = 0; t < L; ++t) {                                 // :107-133
-      const bf16_t* kr = kc + (static_cast<size_t>(kvh) * max_seq + t) * D;
+      const int ct = t < sink_len ? t : tail_start + (t - sink_len);
+      const bf16_t* kr = kc + (static_cast<size_t>(kvh) * max_seq + ct) * D;
       float s = 0.0f;
       for (int d = 0; d < D; ++d) s += qf[d] * bf(kr[d]);
       sc[t] = s * scale;
@@ -102,11 +106,19 @@ static void decode_baseline_one(const bf16_t* q, const bf16_t* kc,
     for (int t = 0; t < L; ++t) sc[t] = sc[t] / sum;              // :152-156
     for (int d = 0; d < D; ++d) {                                 // :158-166
       float acc = 0.0f;
-      for (int t = 0; t < L; ++t)
-        acc += sc[t] * bf(vc[(static_cast<size_t>(kvh) * max_seq + t) * D + d]);
+      for (int t = 0; t < L; ++t) {
+        const int ct = t < sink_len ? t : tail_start + (t - sink_len);
+        acc += sc[t] * bf(vc[(static_cast<size_t>(kvh) * max_seq + ct) * D + d]);
+      }
       out[h * D + d] = orc_f32_to_bf16(acc);
     }
   }
+}
+
+static void decode_baseline_one(const bf16_t* q, const bf16_t* kc,
+                                const bf16_t* vc, bf16_t* out, int Hq,
+                                int Hkv, int D, int max_seq, int L) {
+  decode_baseline_rows(q, kc, vc, out, Hq, Hkv, D, max_seq, 0, 0, L);
 }
 
 void orc_attention_decode_baseline(const bf16_t* q, const bf16_t* kc,
@@ -119,6 +131,35 @@ void orc_attention_decode_baseline(const bf16_t* q, const bf16_t* kc,
                         vc + static_cast<size_t>(b) * Hkv * max_seq * D,
                         out + static_cast<size_t>(b) * Hq * D, Hq, Hkv, D,
                         max_seq, cached_len);
+}
+
+// ops::attention_decode with the decode window knobs (AttentionOps.cpp:
+// 533-551 read them from AILA_ATTN_DECODE_WINDOW / _WINDOW_START / _SINK;
+// the window plan is :598-616) on the baseline kernel, per sequence of
+// lens[b] rows (or cached_len when lens is null). window_start < 0 is the
+// reference's default max(512, window).
+void orc_attention_decode_window(const bf16_t* q, const bf16_t* kc, const bf16_t* vc, bf16_t* out, int B,
+                                 int Hq, int Hkv, int D, int max_seq, int cached_len, const int* lens,
+                                 int window, int window_start, int sink) {
+  if (window_start < 0) window_start = std::max(512, window);
+  for (int b = 0; b < B; ++b) {
+    const int L = lens ? lens[b] : cached_len;
+    const bool apply_window = window > 0 && L > window_start;   // :598
+    int effective_window = L;
+    if (apply_window) effective_window = std::min(L, window);
+    int tail_start = L - effective_window;
+    int sink_len = 0;
+    if (apply_window && sink > 0) sink_len = std::min(sink, std::max(0, L - effective_window));
+    int effective_len = effective_window + sink_len;
+    if (effective_len >= L) {                                    // :612-616
+      tail_start = 0;
+      sink_len = 0;
+      effective_len = L;
+    }
+    decode_baseline_rows(q + static_cast<size_t>(b) * Hq * D, kc + static_cast<size_t>(b) * Hkv * max_seq * D,
+                         vc + static_cast<size_t>(b) * Hkv * max_seq * D, out + static_cast<size_t>(b) * Hq * D, Hq,
+                         Hkv, D, max_seq, tail_start, sink_len, effective_len);
+  }
 }
 
 // attention_decode_exact_head256_partial_merge, AttentionOps.cpp:168-320,

@@ -13,6 +13,8 @@
 extern "C" {
 void orc_attention_decode_baseline(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
                                    int, int, int, int);
+void orc_attention_decode_window(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int,
+                                 int, int, const int*, int, int, int);
 void orc_attention_prefill_naive(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
                                  int, int);
 void orc_attention_prefill_cached(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int,
@@ -170,6 +172,12 @@ int main() {
     ops::attention_decode(ctx, tq, tk, tv, out, scores, Hq, Hkv, D, L, nullptr);
     e = relerr(download<uint16_t>(ctx, out), want);
     expect(e <= 1e-2, "attention_decode (single pass)", e);
+    // decode window with sinks (the AILA_ATTN_DECODE_* knobs as arguments)
+    orc_attention_decode_window(q.data(), kc.data(), vc.data(), want.data(), 1, Hq, Hkv, D, max_seq, L, nullptr,
+                                1000, -1, 6);
+    ops::attention_decode_window(ctx, tq, tk, tv, out, scores, Hq, Hkv, D, L, &partials, 1000, -1, 6);
+    e = relerr(download<uint16_t>(ctx, out), want);
+    expect(e <= 1e-2, "attention_decode_window (window 1000, sink 6)", e);
   }
   // ---- prefill + copy_to_cache, fused variant, cached prefill -------------
   {

@@ -100,12 +100,13 @@ def test_prefill_then_decode_continues_the_state():
 def test_prefill_rejects_bad_args():
     import torch
     import aila_amd
-    q = torch.zeros((1, 8, 2, 64), dtype=torch.bfloat16, device="cuda")
+    # dk = 64 runs the general-shape kernel; head dims above 256 run nowhere
+    q = torch.zeros((1, 8, 2, 320), dtype=torch.bfloat16, device="cuda")
     v = torch.zeros((1, 8, 2, 64), dtype=torch.bfloat16, device="cuda")
     ab = torch.zeros((1, 8, 2), dtype=torch.bfloat16, device="cuda")
-    st = torch.zeros((1, 2, 64, 64), dtype=torch.float32, device="cuda")
+    st = torch.zeros((1, 2, 320, 64), dtype=torch.float32, device="cuda")
     with pytest.raises(aila_amd.AilaHipError):
-        aila_amd.deltanet_prefill(q, q, v, ab, ab, st)     # dk = 64 unsupported
+        aila_amd.deltanet_prefill(q, q, v, ab, ab, st)
 
 
 @pytest.mark.parametrize("decay", [0.9, 0.99, 0.999])
