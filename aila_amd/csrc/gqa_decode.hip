@@ -1026,6 +1026,13 @@ extern "C" int aila_hip_kv_append_paged(const void* k_new, const void* v_new, vo
   AILA_REQUIRE(B > 0 && Hkv > 0 && D > 0 && D % 8 == 0 && page_size > 0 && max_pages > 0,
                "kv_append_paged: bad shape (B=%d Hkv=%d D=%d page_size=%d max_pages=%d)", B, Hkv, D, page_size,
                max_pages);
+  // the same row-range cap as the paged decode (int row arithmetic)
+  AILA_REQUIRE(static_cast<long>(max_pages) * page_size <= (1L << 30),
+               "kv_append_paged: max_pages * page_size = %ld rows exceeds 2^30", static_cast<long>(max_pages) * page_size);
+  // rows move as 16-byte vectors
+  AILA_REQUIRE(reinterpret_cast<uintptr_t>(k_new) % 16 == 0 && reinterpret_cast<uintptr_t>(v_new) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(k_pages) % 16 == 0 && reinterpret_cast<uintptr_t>(v_pages) % 16 == 0,
+               "kv_append_paged: k_new, v_new, k_pages and v_pages must be 16-byte aligned");
   const int n = B * Hkv * (D / 8);
   hipLaunchKernelGGL(kv_append_paged_kernel, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u32x4*>(k_new), static_cast<const u32x4*>(v_new), static_cast<bf16*>(k_pages),

@@ -577,7 +577,12 @@ __global__ __launch_bounds__(256) void gqa_prefill_merge_kernel(const float* __r
     L += w * rec[z * slice + 1];
     acc += w * *reinterpret_cast<const f32x4*>(rec + z * slice + 4 + c);
   }
-  const float inv = 1.0f / L;
+  // Every run of every row is non-empty (the host caps nz at the first query
+  // block's key-block count, so run z of n >= nz blocks holds
+  // floor(n(z+1)/nz) - floor(nz z/nz) >= 1 blocks, and each row's diagonal
+  // key lies in some run): every record is written and L > 0. The guard
+  // keeps a zero row instead of NaN should that ever break.
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
   *reinterpret_cast<u32x2*>(out + static_cast<size_t>(row) * o_row_stride + h * D + c) =
       u32x2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
 }
@@ -591,6 +596,11 @@ int launch_prefill(const bf16* q, const bf16* k, const bf16* v, int kv_row_strid
   const int nqb = (S + C::BM - 1) / C::BM;
   const int npair = (nqb + 1) / 2;
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+  // Each key run must hold at least one key block of every query block, so
+  // that every record the merge reads is written: the first query block has
+  // the fewest key blocks.
+  const int min_blocks = (start_pos + (S < C::BM ? S : C::BM) - 1) / BN + 1;
+  if (nz > min_blocks) nz = min_blocks;
   if (nz < 2) {
     nz = 1;
     part = nullptr;
@@ -658,6 +668,7 @@ int prefill_key_splits(int S, int start_pos, int Hq) {
   if (2 * nwg > resident) return 1;
   const int min_blocks = (start_pos + std::min(C::BM, S) - 1) / PS::BN + 1;   // the first query block's keys
   int nz = (resident + nwg - 1) / nwg;
+  // at least 4 key blocks per run; launch_prefill relies on >= 1
   nz = std::min(nz, std::min(kMaxKeySplits, min_blocks / 4));
   return nz < 2 ? 1 : nz;
 }

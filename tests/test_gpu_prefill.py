@@ -155,6 +155,40 @@ def test_prefill_cached_key_split(S, start, Hq, Hkv, D):
         assert np.max(rows) <= 2 * ATTN_TOL, nbytes
 
 
+@pytest.mark.parametrize("S,Hq,Hkv,D", [(64, 16, 4, 256), (100, 32, 8, 128), (50, 8, 1, 64)])
+def test_prefill_cached_key_split_at_its_limits(S, Hq, Hkv, D):
+    """The key split at the smallest cached prefix that still splits (two
+    runs of the fewest key blocks a run may hold) and at the smallest prefix
+    that reaches the run cap: the merge reads only records every run wrote."""
+    import torch
+    import aila_amd
+    per_run = Hq * S * (D + 4) * 4
+    runs = [aila_amd.gqa_prefill_cached_workspace_size(S, st, Hq, Hkv, D) // per_run for st in range(0, 6000)]
+    cases = []
+    if any(r >= 2 for r in runs):
+        cases.append(next(st for st, r in enumerate(runs) if r >= 2))
+    cap = max(runs)
+    if cap > 2:
+        cases.append(next(st for st, r in enumerate(runs) if r == cap))
+    assert cases, "some prefix should split"
+    for start in cases:
+        print(f"key split limit S={S} start={start} runs={runs[start]} D={D}", flush=True)
+        max_seq = start + S + 3
+        seed = 7400 + start + D
+        kc = dg.normal_bf16(seed, 1, (Hkv, max_seq, D))
+        vc = dg.normal_bf16(seed, 2, (Hkv, max_seq, D))
+        kc[:, start + S:] = 0x7FC0
+        vc[:, start + S:] = 0x7FC0
+        q = dg.normal_bf16(seed, 0, (S, Hq * D))
+        want = dg.bf16_to_f32(oracle.attention_prefill_cached(q, kc, vc, S, start, Hq, Hkv, D, max_seq))
+        ws = torch.full((runs[start] * per_run // 4,), float("nan"), dtype=torch.float32,
+                        device="cuda").view(torch.uint8)
+        got = dg.bf16_to_f32(_np(aila_amd.gqa_prefill_cached(_t(q), _t(kc), _t(vc), start, Hq, workspace=ws)))
+        torch.cuda.synchronize()
+        assert np.isfinite(got).all(), start
+        assert _relerr(got, want) <= ATTN_TOL, start
+
+
 def test_prefill_cached_no_split_for_long_turns():
     import aila_amd
     # a 2048-token turn already fills the device: no workspace wanted

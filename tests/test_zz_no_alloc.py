@@ -86,3 +86,58 @@ def test_noalloc_rejects_sizes_beyond_the_scratch():
     rc = lib.aila_hip_gqa_decode_noalloc(p, p, p, p, B, Hq, 4, D, 1024, 100, None, None)
     assert rc == -1
     assert b"scratch" in lib.aila_hip_last_error()
+
+
+_CAPTURE_SCRIPT = r'''
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+import aila_amd
+from aila_amd import datagen as dg
+lib = aila_amd.lib()
+B, Hq, Hkv, D, max_seq, L = 2, 16, 4, 256, 4096, 4000
+def t(x):
+    return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).cuda()
+q = t(dg.normal_bf16(0x0A13, 0, (B, Hq, D)))
+kc = t(dg.normal_bf16(0x0A13, 1, (B, Hkv, max_seq, D)))
+vc = t(dg.normal_bf16(0x0A13, 2, (B, Hkv, max_seq, D)))
+lens = torch.tensor([4000, 2500], dtype=torch.int32, device="cuda")
+out_g = torch.empty_like(q)
+p = lambda x: ctypes.c_void_p(x.data_ptr())
+s = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.stream(s):
+    with torch.cuda.graph(g, stream=s):
+        # the first no-alloc call of this process: its scratch lookup happens here
+        rc = lib.aila_hip_gqa_decode_noalloc(p(q), p(kc), p(vc), p(out_g), B, Hq, Hkv, D, max_seq, L, p(lens),
+                                             ctypes.c_void_p(s.cuda_stream))
+assert rc == 0, lib.aila_hip_last_error()
+ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+ref = aila_amd.gqa_decode(q, kc, vc, L, workspace=ws, seq_lens=lens)
+torch.cuda.synchronize()
+for i in range(3):
+    out_g.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out_g, ref), f"replay {i} differs"
+    lens[1] = 2500 - 100 * (i + 1)          # eager work between replays: a shorter sequence
+    ref = aila_amd.gqa_decode(q, kc, vc, L, workspace=ws, seq_lens=lens)
+    torch.cuda.synchronize()
+print("CAPTURE_OK")
+'''
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """The scratch address is looked up on a device's first no-alloc call;
+    here that first call is made under HIP graph capture (a fresh process),
+    and the captured launch replays bit-exact against the workspace entry
+    point, with the sequence lengths changed between replays."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("noalloc first call under capture (subprocess)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0 and "CAPTURE_OK" in r.stdout, r.stdout + r.stderr
