@@ -248,12 +248,15 @@ __device__ __forceinline__ RowPos rope_row_pos(const RopePos& rp, int b, int row
   return p;
 }
 
-// Position rotating frequency index j (0 <= j < rot/2).
-__device__ __forceinline__ float rope_freq_pos(const RowPos& p, int j) {
+// Position rotating frequency index j (0 <= j < rot/2). Selects on values
+// (a branch that returns different members would make the compiler address
+// the struct through memory, and it then lives in LDS).
+__device__ __forceinline__ float rope_freq_pos(RowPos p, int j) {
   const int m = j % 3, q = j / 3;
-  if (m == 1 && q < p.sec_h) return static_cast<float>(p.h);
-  if (m == 2 && q < p.sec_w) return static_cast<float>(p.w);
-  return static_cast<float>(p.t);
+  int v = p.t;
+  v = (m == 1 && q < p.sec_h) ? p.h : v;
+  v = (m == 2 && q < p.sec_w) ? p.w : v;
+  return static_cast<float>(v);
 }
 
 }  // namespace aila

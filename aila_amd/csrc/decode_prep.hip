@@ -52,7 +52,7 @@ __device__ __forceinline__ void norm_head_to_lds(const bf16* __restrict__ x, con
 // index j rotates at rope_freq_pos(rp, j) (the row's position, or its mRoPE
 // stream).
 template <int D>
-__device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restrict__ y, int rot, const RowPos& rp,
+__device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restrict__ y, int rot, RowPos rp,
                                               float theta) {
   constexpr int E = D / 64;
   const int lane = threadIdx.x & 63;

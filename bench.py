@@ -182,6 +182,106 @@ def bench_config5(torch, aila_amd, steps, warmup):
                 dn_step_bytes=(N_LAYERS - N_GQA) * dn_b, L_first=L_first, W=W)
 
 
+def bench_config5_full_layers(torch, aila_amd, W, steps, warmup):
+    """The config-5 step as the hybrid backend runs each layer
+    (Qwen35HybridTextBackend.cpp:2109-2180 and :975-1166): every GQA layer is
+    one launch of QK-norm + partial RoPE (rotary 64) + K/V append + split-K
+    decode + the sigmoid(gate) epilogue from the packed q|gate projection
+    (gqa_decode_prepare_append, packed_gate=2); every DeltaNet layer is the
+    whole layer from the fused [qkv | z | a | b] row: conv1d ring + SiLU, L2
+    norms, the recurrence and RMSNorm(o) * w * SiLU(z) (deltanet_layer_decode,
+    one workgroup per value head). Same caches and states as the headline
+    step; the conv ring heads and positions advance inside the graph."""
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xA11A + 9)
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    d, Hk, Hv = DN_D, DN_HK, DN_HV
+    ch = 2 * Hk * d + Hv * d
+    row = ch + Hv * d + 2 * Hv
+    n_dn = N_LAYERS - N_GQA
+    conv_w = [torch.randn((ch, 4), generator=gen, **bf) * 0.5 for _ in range(n_dn)]
+    rings = [torch.empty((B5, 3, ch), **f32).normal_(generator=gen) for _ in range(n_dn)]
+    norm_w = [1.0 + 0.1 * torch.randn(d, generator=gen, **f32) for _ in range(n_dn)]
+    arrivals = [torch.zeros((B5 * Hk,), dtype=torch.int32, device=dev) for _ in range(n_dn)]
+    qn_w = [torch.randn(GQA_D, generator=gen, **bf) for _ in range(N_GQA)]
+    kn_w = [torch.randn(GQA_D, generator=gen, **bf) for _ in range(N_GQA)]
+    pool = []
+    for _ in range(NPOOL):
+        layers = []
+        for layer in range(N_LAYERS):
+            if layer % 4 == 3:
+                layers.append(dict(q=torch.randn((B5, GQA_HQ, 2 * GQA_D), generator=gen, **bf),
+                                   k=torch.randn((B5, GQA_HKV, GQA_D), generator=gen, **bf),
+                                   v=torch.randn((B5, GQA_HKV, GQA_D), generator=gen, **bf)))
+            else:
+                layers.append(dict(row=torch.randn((B5, row), generator=gen, **bf)))
+        pool.append(layers)
+    gqa_out = torch.empty((B5, GQA_HQ, GQA_D), **bf)
+    dn_out = torch.empty((B5, Hv * d), **bf)
+    heads = torch.zeros((B5,), dtype=torch.int32, device=dev)
+    positions = torch.full((B5,), L5, dtype=torch.int32, device=dev)
+
+    def step(p):
+        gi = di = 0
+        for layer in range(N_LAYERS):
+            x = pool[p][layer]
+            if layer % 4 == 3:
+                aila_amd.gqa_decode_prepare_append(x["q"], x["k"], x["v"], W["kc"][gi], W["vc"][gi],
+                                                   W["max_seq"] - 1, q_norm_w=qn_w[gi], k_norm_w=kn_w[gi],
+                                                   rotary_dim=64, theta=1e7, packed_gate=True, apply_gate=True,
+                                                   out=gqa_out, workspace=W["ws"], positions=positions)
+                gi += 1
+            else:
+                r = x["row"]
+                aila_amd.deltanet_layer_decode(r[:, :ch], r[:, ch:ch + Hv * d], r[:, ch + Hv * d:ch + Hv * d + Hv],
+                                               r[:, ch + Hv * d + Hv:], conv_w[di], rings[di], 0, norm_w[di],
+                                               W["states"][di], Hk, out=dn_out, conv_heads=heads,
+                                               arrivals=arrivals[di])
+                di += 1
+        positions.add_(1)
+        heads.add_(1).remainder_(3)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    positions.fill_(L5)
+    graphs = []
+    for p in range(NPOOL):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(p)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs[i % NPOOL].replay()
+    torch.cuda.synchronize()
+    L_first = int(positions[0].item()) + 1
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(steps):
+        graphs[(warmup + i) % NPOOL].replay()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    L_mean = L_first + (steps - 1) / 2.0
+    # GQA layer: K/V rows read, packed q|gate in, k/v in, k/v rows written, out
+    gqa_b = (2 * B5 * GQA_HKV * L_mean * GQA_D * 2 + B5 * GQA_HQ * 2 * GQA_D * 2 + 2 * B5 * GQA_HKV * GQA_D * 2 * 2
+             + B5 * GQA_HQ * GQA_D * 2)
+    dn_b = deltanet_layer_bytes(B5, Hk, Hv, d)
+    step_bytes = N_GQA * gqa_b + n_dn * dn_b
+    del graphs, pool, rings
+    return {"config": ("config-5 stack, each layer as the backend runs it: GQA = norm + RoPE(64) + append + "
+                       "split-K decode + sigmoid(gate) in one launch; DeltaNet = conv ring + SiLU + norms + "
+                       "recurrence + gated RMSNorm in one launch"),
+            "ms_per_step": round(ms, 4), "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "step_bytes": int(step_bytes), "context": L_first, "steps": steps}
+
+
 def roofline_gqa(torch, aila_amd, W, reps=64):
     """Dominant kernel: one GQA decode launch (split + merge dispatch) on a
     config-5 layer at L = 32768, timed with HIP events around a batch of
@@ -209,15 +309,76 @@ def roofline_gqa(torch, aila_amd, W, reps=64):
     avg_ms = s.elapsed_time(e) / reps
     byts = gqa_bytes(B5, GQA_HQ, GQA_HKV, GQA_D, L)
     achieved = byts / (avg_ms * 1e-3) / 1e9
-    traffic = None
+    # HBM bytes per launch from the committed counter runs, used only while
+    # the kernel source they were measured on is unchanged (source stamp).
+    traffic, note = None, "no counter profile"
     tpath = os.path.join(ROOT, "profiles", "gqa_decode_config5_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            prof = json.load(f)
+        if prof.get("source_sha16") == decode_source_stamp():
+            traffic = prof.get("hbm_bytes_per_launch")
+            note = "rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel source, calibrated on a 1 GiB copy"
+        else:
+            note = "counter profile is stale (kernel source changed since it was measured)"
     return {"kernel": "gqa_decode_split_kernel<256,4> + merge", "bound": "hbm",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": note,
             "algorithmic_bytes": byts, "avg_launch_us": round(avg_ms * 1e3, 2)}
+
+
+def decode_source_stamp():
+    """First 16 hex digits of the SHA-256 of the GQA decode kernel sources."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in ("gqa_decode.hip", "common.hpp"):
+        with open(os.path.join(ROOT, "aila_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def write_traffic(fetch_csv, write_csv):
+    """Builds profiles/gqa_decode_config5_traffic.json from the two
+    `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of
+    `bench.py --profile-kernel gqa_decode` (their run_counter_collection.csv):
+    medians per kernel, scaled by what each counter reads for the 1 GiB
+    device copy of the same run (1 GiB read, 1 GiB written)."""
+    import csv
+
+    def medians(path):
+        vals = {}
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return {k: statistics.median(v) for k, v in vals.items()}
+
+    def pick(m, key):
+        names = [k for k in m if key in k]
+        if not names:
+            raise SystemExit(f"no dispatch of a kernel named *{key}* in the counter file")
+        return max(names, key=lambda k: m[k])
+
+    F, Wr = medians(fetch_csv), medians(write_csv)
+    gib_kib = float(1 << 20)
+    cf, cw = pick(F, "copy"), pick(Wr, "copy")
+    fs, ws_ = gib_kib / F[cf], gib_kib / Wr[cw]
+    sk, mk = pick(F, "gqa_decode_split_kernel"), pick(F, "gqa_decode_merge_kernel")
+    fetch = {"split": F[sk], "merge": F[mk]}
+    write = {"split": Wr[pick(Wr, "gqa_decode_split_kernel")], "merge": Wr[pick(Wr, "gqa_decode_merge_kernel")]}
+    hbm = int(round(1024 * (fs * (fetch["split"] + fetch["merge"]) + ws_ * (write["split"] + write["merge"]))))
+    out = {"kernel": "gqa_decode_split_kernel<256,4> + gqa_decode_merge_kernel<256>",
+           "workload": "config 5 GQA layer: B=8 Hq=16 Hkv=4 D=256 L=32768",
+           "fetch_kib": {k: round(v, 1) for k, v in fetch.items()},
+           "write_kib": {k: round(v, 1) for k, v in write.items()},
+           "fetch_scale": round(fs, 4), "write_scale": round(ws_, 4),
+           "hbm_bytes_per_launch": hbm,
+           "algorithmic_bytes_per_launch": gqa_bytes(B5, GQA_HQ, GQA_HKV, GQA_D, L5),
+           "source_sha16": decode_source_stamp(),
+           "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE -- python3 bench.py --profile-kernel gqa_decode"}
+    with open(os.path.join(ROOT, "profiles", "gqa_decode_config5_traffic.json"), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(json.dumps(out))
 
 
 def profile_kernel(torch, aila_amd, reps=20):
@@ -719,7 +880,10 @@ def cpu_baseline(min_seconds=10.0):
             "sample": (f"oracle/liboracle_fast.so (-O3 -ffast-math, OpenMP {threads} threads): one config-5 "
                        f"layer group (1 GQA layer split-K tile 128 + 3 DeltaNet layers), batch 1, L={L}; "
                        f"median of {len(times)} runs ({sum(times):.1f} s)"),
-            "seconds_per_group": round(t, 4)}
+            "seconds_per_group": round(t, 4),
+            "config5_step_extrapolation": (
+                f"the config-5 step is 8 such groups for each of 8 sequences: {64 * t:.2f} s per step at this "
+                "rate (work and bytes both scale linearly with layers and batch, so the GB/s is the same)")}
 
 
 def cpu_model():
@@ -805,7 +969,12 @@ def main():
                              "stack", "prefill_cached"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
+    ap.add_argument("--write-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/gqa_decode_config5_traffic.json from the two counter runs and exit")
     args = ap.parse_args()
+    if args.write_traffic:
+        write_traffic(*args.write_traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the path "
               "has no multi-GPU mode in this build.", file=sys.stderr)
@@ -836,9 +1005,11 @@ def main():
     log(f"[bench] config 5: {r5['ms']:.3f} ms/step, {value:.0f} GB/s")
     roof = roofline_gqa(torch, aila_amd, r5["W"])
     log(f"[bench] roofline gqa_decode: {roof['achieved']} GB/s ({roof['frac']*100:.1f}%)")
+    full = bench_config5_full_layers(torch, aila_amd, r5["W"], args.steps, args.warmup)
+    log(f"[bench] config 5 with whole layers: {full['ms_per_step']} ms/step, {full['GBps']} GB/s")
     del r5["W"]
     torch.cuda.empty_cache()
-    sub = {}
+    sub = {"config5_full_layers": full}
     if not args.no_sub:
         sub["gqa_prefill"] = sub_prefill(torch, aila_amd)
         log(f"[bench] prefill {sub['gqa_prefill']}")
