@@ -966,7 +966,7 @@ def main():
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
                     choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill", "paged_decode",
                              "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode",
-                             "stack", "prefill_cached"],
+                             "stack", "stack_full", "prefill_cached"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     ap.add_argument("--write-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -995,7 +995,9 @@ def main():
          "paged_decode": lambda t, a: sub_paged_decode(t, a),
          "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a),
          "prefill_cached": lambda t, a: sub_prefill_cached(t, a),
-         "stack": lambda t, a: {k: v for k, v in bench_config5(t, a, 32, 4).items() if k != "W"}}[args.profile_kernel](torch, aila_amd)
+         "stack": lambda t, a: {k: v for k, v in bench_config5(t, a, 32, 4).items() if k != "W"},
+         "stack_full": lambda t, a: bench_config5_full_layers(t, a, build_config5(t, a, 32, 4), 32, 4),
+         }[args.profile_kernel](torch, aila_amd)
         if r:
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
         return
