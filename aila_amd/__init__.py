@@ -123,14 +123,18 @@ class RopePos(ctypes.Structure):
     _fields_ = [("interleaved", _I), ("pos_t", _P), ("pos_h", _P), ("pos_w", _P),
                 ("pos_stride", _I), ("prompt_pos_len", _I), ("text_pos_delta", _I),
                 ("prompt_pos_lens", _P), ("text_pos_deltas", _P),
-                ("mrope_section_t", _I), ("mrope_section_h", _I), ("mrope_section_w", _I)]
+                ("mrope_section_t", _I), ("mrope_section_h", _I), ("mrope_section_w", _I),
+                ("inv_freq", _P)]
 
 
 def rope_pos(prompt_pos_len: int = 0, text_pos_delta: int = 0, pos_t=None, pos_h=None, pos_w=None,
-             interleaved: bool = True, sections=(0, 0, 0), prompt_pos_lens=None, text_pos_deltas=None):
+             interleaved: bool = True, sections=(0, 0, 0), prompt_pos_lens=None, text_pos_deltas=None,
+             inv_freq=None):
     """Rotary position record. pos_t/pos_h/pos_w: device int32 [P] (one prompt,
     shared by every sequence) or [B, P] (per sequence); prompt_pos_lens /
-    text_pos_deltas: optional device int32 [B] overriding the scalars."""
+    text_pos_deltas: optional device int32 [B] overriding the scalars;
+    inv_freq: optional device float32 [rotary_dim/2] table (pair d rotates by
+    position * inv_freq[d])."""
     import torch
     rp = RopePos()
     rp.interleaved = int(bool(interleaved))
@@ -158,6 +162,10 @@ def rope_pos(prompt_pos_len: int = 0, text_pos_delta: int = 0, pos_t=None, pos_h
         rp.prompt_pos_lens = prompt_pos_lens.data_ptr()
     if text_pos_deltas is not None:
         rp.text_pos_deltas = text_pos_deltas.data_ptr()
+    if inv_freq is not None:
+        _need(inv_freq, torch.float32, tuple(inv_freq.shape), "inv_freq", align=4)
+        keep.append(inv_freq)
+        rp.inv_freq = inv_freq.data_ptr()
     rp._keep = keep   # the device arrays must outlive the launches that read them
     return rp
 

@@ -42,4 +42,4 @@ int load_rope_pos(const aila_hip_rope_pos* rp, aila_hip_rope_pos* out, const cha
 
 extern "C" const char* aila_hip_last_error(void) { return aila::g_last_error; }
 
-extern "C" int aila_hip_version(void) { return (1 << 16) | 1; }
+extern "C" int aila_hip_version(void) { return (1 << 16) | 2; }

@@ -248,6 +248,12 @@ __device__ __forceinline__ RowPos rope_row_pos(const RopePos& rp, int b, int row
   return p;
 }
 
+// Inverse frequency of rotary pair j: the caller's table, or
+// theta^(-2j/rot).
+__device__ __forceinline__ float rope_inv_freq(const RopePos& rp, int j, int rot, float theta) {
+  return rp.inv_freq ? rp.inv_freq[j] : 1.0f / powf(theta, (2.0f * j) / static_cast<float>(rot));
+}
+
 // Position rotating frequency index j (0 <= j < rot/2). Selects on values
 // (a branch that returns different members would make the compiler address
 // the struct through memory, and it then lives in LDS).

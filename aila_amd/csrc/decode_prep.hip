@@ -53,7 +53,7 @@ __device__ __forceinline__ void norm_head_to_lds(const bf16* __restrict__ x, con
 // stream).
 template <int D>
 __device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restrict__ y, int rot, RowPos rp,
-                                              float theta) {
+                                              float theta, const float* __restrict__ inv_freq) {
   constexpr int E = D / 64;
   const int lane = threadIdx.x & 63;
   const int half = rot / 2;
@@ -63,7 +63,7 @@ __device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restri
     float r = s_row[d];
     if (d < rot) {
       const int dd = d < half ? d : d - half;                 // frequency index
-      const float freq = 1.0f / powf(theta, (2.0f * dd) / static_cast<float>(rot));
+      const float freq = inv_freq ? inv_freq[dd] : 1.0f / powf(theta, (2.0f * dd) / static_cast<float>(rot));
       const float ang = rope_freq_pos(rp, dd) * freq;
       const float c = cosf(ang), s = sinf(ang);
       r = d < half ? s_row[d] * c - s_row[d + half] * s : s_row[d] * c + s_row[d - half] * s;
@@ -92,14 +92,14 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(
     }
     norm_head_to_lds<D>(src, qn_w, eps, s_row);
     __syncthreads();
-    rope_from_lds<D>(s_row, dst, rot, rp, theta);
+    rope_from_lds<D>(s_row, dst, rot, rp, theta, ropep.inv_freq);
     return;
   }
   const int h = hh - Hq;
   bf16* kr = k + (static_cast<size_t>(b) * Hkv + h) * D;
   norm_head_to_lds<D>(kr, kn_w, eps, s_row);
   __syncthreads();
-  rope_from_lds<D>(s_row, kr, rot, rp, theta);
+  rope_from_lds<D>(s_row, kr, rot, rp, theta, ropep.inv_freq);
   if (k_cache && p >= 0 && p < max_seq) {
     // each lane re-reads only the elements it wrote itself
     const size_t row = ((static_cast<size_t>(b) * Hkv + h) * max_seq + p) * D;
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(64) void rope_kernel(bf16* __restrict__ q, bf16* __
   const int lane = threadIdx.x;
   for (int d = lane; d < D; d += 64) s_row[d] = bf2f(row[d]);
   __syncthreads();
-  rope_from_lds<D>(s_row, row, rot, rope_row_pos(ropep, 0, start_pos + s), theta);
+  rope_from_lds<D>(s_row, row, rot, rope_row_pos(ropep, 0, start_pos + s), theta, ropep.inv_freq);
 }
 
 // o = in * sigmoid(g), 8 elements per thread where n allows.

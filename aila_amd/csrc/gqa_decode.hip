@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const int half = pa.rot / 2;
     const RowPos rp = rope_row_pos(pa.rope, b, len - 1);
     for (int j = threadIdx.x; j < half; j += kThreads) {
-      const float freq = 1.0f / powf(pa.theta, (2.0f * j) / static_cast<float>(pa.rot));
+      const float freq = rope_inv_freq(pa.rope, j, pa.rot, pa.theta);
       const float ang = rope_freq_pos(rp, j) * freq;
       s_tab[2 * j] = cosf(ang);
       s_tab[2 * j + 1] = sinf(ang);
@@ -371,6 +371,11 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   }
 
   if (!early && t0 < s1) dma_k(0, t0, pg_cur);
+  // The loop reads a chunk's K stage at its top; every iteration waits for
+  // its own DMA at its end, and this wait covers the first chunk. The
+  // compiler does not order that first LDS read after the DMA by itself: the
+  // rotated loop of the fused-preparation kernel read the stage before it
+  // landed (stale LDS from the previous workgroup).
   int pg_nxt = page_of(t0 + kWaves * kChunk);
   for (int it = 0; t0 < s1; ++it, t0 += kWaves * kChunk) {
     const int stage = it & 1;

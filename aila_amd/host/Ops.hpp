@@ -125,9 +125,9 @@ void apply_rope_partial(Context& ctx, Tensor& q, Tensor& k, int seq_len, int sta
 
 // One-token QK-norm + RoPE + K/V append (Ops.hpp:205-211). q [1, Hq*D] and
 // k [1, Hkv*D] are updated in place; the caches are [Hkv, max_seq, D]
-// (max_seq from k_cache.shape(1)). rope_freq is accepted and unused: the
-// backends fill it with 1/theta^(2d/head_dim) (Qwen3DenseBackend.cpp:232-236),
-// which the kernel computes itself from theta.
+// (max_seq from k_cache.shape(1)). Pair d rotates by start_pos * rope_freq[d]
+// (f32 [head_dim/2]; the backends fill it with 1/theta^(2d/head_dim),
+// Qwen3DenseBackend.cpp:232-236); an invalid rope_freq tensor uses theta.
 void decode_prepare_qkv(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& rope_freq,
                         Tensor& q_norm_weight, Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache,
                         int start_pos, int num_heads_q, int num_kv_heads, int head_dim, float eps,

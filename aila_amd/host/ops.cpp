@@ -240,9 +240,20 @@ void decode_prepare_qkv(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& r
                         Tensor& q_norm_weight, Tensor& k_norm_weight, Tensor& k_cache, Tensor& v_cache,
                         int start_pos, int num_heads_q, int num_kv_heads, int head_dim, float eps,
                         float theta) {
-  (void)rope_freq;
-  decode_prepare_qkv_partial(ctx, q, k, v, q_norm_weight, k_norm_weight, k_cache, v_cache, start_pos,
-                             num_heads_q, num_kv_heads, head_dim, eps, head_dim, theta);
+  // angle = start_pos * rope_freq[d] (ElementwiseOps.cpp:159, 198): the
+  // table is used as given (an invalid tensor falls back to theta)
+  for (Tensor* t : {&q, &k, &v, &k_cache, &v_cache}) need_dtype(*t, DType::bf16, "decode_prepare_qkv");
+  aila_hip_rope_pos rp{};
+  if (rope_freq.valid()) {
+    need_dtype(rope_freq, DType::f32, "decode_prepare_qkv rope_freq");
+    if (rope_freq.numel() < head_dim / 2) throw std::runtime_error("decode_prepare_qkv: rope_freq holds < head_dim/2 values");
+    rp.inv_freq = rope_freq.data_as<float>();
+  }
+  check(aila_hip_decode_prepare_qkv(q.data(), 0, q.data(), nullptr, k.data(), v.data(), opt(q_norm_weight),
+                                    opt(k_norm_weight), k_cache.data(), v_cache.data(), 1, num_heads_q,
+                                    num_kv_heads, head_dim, static_cast<int>(k_cache.shape(1)), head_dim, theta,
+                                    eps, start_pos, nullptr, &rp, ctx.stream()),
+        "decode_prepare_qkv");
 }
 
 void decode_prepare_qkv_partial(Context& ctx, Tensor& q, Tensor& k, Tensor& v, Tensor& q_norm_weight,

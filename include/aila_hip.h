@@ -54,7 +54,11 @@ int aila_hip_version(void);
  * P entries per sequence; mrope_section_t is accepted and, as in the
  * reference, unused. A zero-initialised struct (or a NULL pointer where an
  * entry point takes one) means "rotate at the cache row". The cache row a
- * decode step appends to is never shifted. */
+ * decode step appends to is never shifted.
+ * inv_freq (optional device float[rotary_dim/2]): pair d rotates by
+ * position * inv_freq[d] instead of position * theta^(-2d/rotary_dim) -- the
+ * backend's precomputed rope_freq table of ops::decode_prepare_qkv
+ * (ElementwiseOps.cpp:105-216, angle = start_pos * rope_freq[d]). */
 typedef struct aila_hip_rope_pos {
   int interleaved;
   const int* pos_t;
@@ -66,6 +70,7 @@ typedef struct aila_hip_rope_pos {
   const int* prompt_pos_lens; /* optional device int[B] */
   const int* text_pos_deltas; /* optional device int[B] */
   int mrope_section_t, mrope_section_h, mrope_section_w;
+  const float* inv_freq;      /* optional device float[rotary_dim/2] */
 } aila_hip_rope_pos;
 
 /* ---------------------------------------------------------------- GQA --- */

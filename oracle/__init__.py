@@ -38,6 +38,7 @@ _SIGS = {
     "orc_attention_f64": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "orc_head_rms_norm": [_P, _P, _P, _F, _I, _I, _I],
     "orc_apply_rope": [_P, _P, _I, _I, _I, _I, _I, _I, _F],
+    "orc_decode_prepare_qkv_freq": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I],
     "orc_apply_rope_partial": [_P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _I, _I, _I, _I, _I],
     "orc_decode_prepare_rp": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                               _I, _I, _I, _I, _I, _I, _F, _F, _P,
@@ -202,6 +203,18 @@ def decode_prepare_qkv(q, k, v, qn_w, kn_w, kc, vc, start_pos, Hq, Hkv, D, eps, 
     assert kc.dtype == U16 and vc.dtype == U16
     lib().orc_decode_prepare_qkv(_p(q), _p(k), _p(v), _p(qn_w), _p(kn_w), _p(kc), _p(vc),
                                  start_pos, Hq, Hkv, D, eps, theta, max_seq)
+    return q, k
+
+
+def decode_prepare_qkv_freq(q, k, v, rope_freq, qn_w, kn_w, kc, vc, start_pos, Hq, Hkv, D, eps, max_seq):
+    """decode_prepare_qkv with the backend's rope_freq table (one sequence);
+    returns (q, k); kc/vc (uint16 arrays or None) are updated."""
+    q = np.array(q, dtype=U16, copy=True, order="C")
+    k = np.array(k, dtype=U16, copy=True, order="C")
+    v, qn_w, kn_w = _c(v, U16), _c(qn_w, U16), _c(kn_w, U16)
+    f = np.ascontiguousarray(rope_freq, dtype=F32)
+    lib().orc_decode_prepare_qkv_freq(_p(q), _p(k), _p(v), _p(f), _p(qn_w), _p(kn_w), _p(kc), _p(vc),
+                                      start_pos, Hq, Hkv, D, eps, max_seq)
     return q, k
 
 

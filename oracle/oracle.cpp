@@ -527,6 +527,34 @@ void orc_decode_prepare_qkv(bf16_t* q, bf16_t* k, const bf16_t* v,
   orc_copy_to_cache(v, vc, 1, start_pos, Hkv, D, max_seq);
 }
 
+// decode_prepare_qkv with the backend's frequency table, as the reference
+// computes it (ElementwiseOps.cpp:105-216): per head RMSNorm (bf16 round),
+// then pair d of q and k rotated by angle = start_pos * rope_freq[d] over the
+// full head (bf16 round), then k, v appended at start_pos. One sequence:
+// q [Hq, D], k/v [Hkv, D] (q, k in place), caches [Hkv, max_seq, D].
+void orc_decode_prepare_qkv_freq(bf16_t* q, bf16_t* k, const bf16_t* v, const float* rope_freq,
+                                 const bf16_t* qn_w, const bf16_t* kn_w, bf16_t* kc, bf16_t* vc, int start_pos,
+                                 int Hq, int Hkv, int D, float eps, int max_seq) {
+  orc_head_rms_norm(q, qn_w, nullptr, eps, 1, Hq, D);
+  orc_head_rms_norm(k, kn_w, nullptr, eps, 1, Hkv, D);
+  const int half = D / 2;
+  auto rotate = [&](bf16_t* x) {
+    for (int d = 0; d < half; ++d) {
+      const float angle = static_cast<float>(start_pos) * rope_freq[d];   // :159, :198
+      const float c = std::cos(angle), sn = std::sin(angle);
+      const float x0 = bf(x[d]), x1 = bf(x[d + half]);
+      x[d] = orc_f32_to_bf16(x0 * c - x1 * sn);
+      x[d + half] = orc_f32_to_bf16(x1 * c + x0 * sn);
+    }
+  };
+  for (int h = 0; h < Hq; ++h) rotate(q + static_cast<size_t>(h) * D);
+  for (int h = 0; h < Hkv; ++h) rotate(k + static_cast<size_t>(h) * D);
+  if (kc) {
+    orc_copy_to_cache(k, kc, 1, start_pos, Hkv, D, max_seq);
+    orc_copy_to_cache(v, vc, 1, start_pos, Hkv, D, max_seq);
+  }
+}
+
 // decode_prepare_qkv_partial (ElementwiseOps.cpp:555-705) and
 // decode_prepare_qgkv_packed_partial (:707-863), batched over B independent
 // sequences (the reference runs one): per head, q (the first D of a packed

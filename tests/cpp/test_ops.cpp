@@ -25,6 +25,8 @@ void orc_deltanet_recurrent(const uint16_t*, const uint16_t*, const uint16_t*, c
                             int, int, int, int, int, float, float, int);
 void orc_head_rms_norm(uint16_t*, const uint16_t*, const float*, float, int, int, int);
 void orc_apply_rope(uint16_t*, uint16_t*, int, int, int, int, int, int, float);
+void orc_decode_prepare_qkv_freq(uint16_t*, uint16_t*, const uint16_t*, const float*, const uint16_t*,
+                                 const uint16_t*, uint16_t*, uint16_t*, int, int, int, int, float, int);
 void orc_apply_rope_partial(uint16_t*, uint16_t*, int, int, int, int, int, int, float, int, const int*, const int*,
                             const int*, int, int, int, int, int);
 void orc_decode_prepare_rp(const uint16_t*, int, uint16_t*, uint16_t*, uint16_t*, const uint16_t*, const uint16_t*,
@@ -87,6 +89,13 @@ static Tensor upload(Context& ctx, const std::vector<T>& h, std::vector<int64_t>
   Tensor t = Tensor::allocate(ctx, shape, dt);
   ctx.memcpy_h2d(t.data(), h.data(), h.size() * sizeof(T));
   return t;
+}
+
+// The backends' rope_freq table, 1/theta^(2d/head_dim) (Qwen3DenseBackend.cpp:232-236).
+static Tensor rope_freq_table(Context& ctx, int D, float theta) {
+  std::vector<float> tab(D / 2);
+  for (int d = 0; d < D / 2; ++d) tab[d] = 1.0f / std::pow(theta, (2.0f * d) / float(D));
+  return upload(ctx, tab, {D / 2}, DType::f32);
 }
 template <typename T>
 static std::vector<T> download(Context& ctx, Tensor& t) {
@@ -316,7 +325,7 @@ int main() {
     // full rotary, q in place
     u16v q1 = rand_bf16(size_t(Hq) * D), k1 = rand_bf16(size_t(Hkv) * D);
     Tensor tq1 = upload(ctx, q1, {1, Hq * D}, DType::bf16), tk1 = upload(ctx, k1, {1, Hkv * D}, DType::bf16);
-    Tensor freq = Tensor::allocate(ctx, {D / 2}, DType::f32);
+    Tensor freq = rope_freq_table(ctx, D, theta);
     ops::decode_prepare_qkv(ctx, tq1, tk1, tv, freq, tqw, tkw, kc, vc, 7, Hq, Hkv, D, eps, theta);
     u16v wq1(size_t(Hq) * D), wk1 = k1;
     const int p7 = 7;
@@ -324,6 +333,19 @@ int main() {
                        nullptr, 1, Hq, Hkv, D, 0, D, theta, eps, &p7);
     e = std::fmax(relerr(download<uint16_t>(ctx, tq1), wq1), relerr(download<uint16_t>(ctx, tk1), wk1));
     expect(e <= 1e-2, "decode_prepare_qkv", e);
+    // a rope_freq table that is not theta's: used as given
+    {
+      std::vector<float> tab(D / 2);
+      for (int d = 0; d < D / 2; ++d) tab[d] = (d % 3 == 0 ? 0.5f : 1.0f) / std::pow(theta, (2.0f * d) / float(D));
+      Tensor tfreq = upload(ctx, tab, {D / 2}, DType::f32);
+      u16v q2 = rand_bf16(size_t(Hq) * D), k2 = rand_bf16(size_t(Hkv) * D);
+      Tensor tq2 = upload(ctx, q2, {1, Hq * D}, DType::bf16), tk2 = upload(ctx, k2, {1, Hkv * D}, DType::bf16);
+      ops::decode_prepare_qkv(ctx, tq2, tk2, tv, tfreq, tqw, tkw, kc, vc, 9, Hq, Hkv, D, eps, theta);
+      orc_decode_prepare_qkv_freq(q2.data(), k2.data(), v.data(), tab.data(), qw.data(), kw.data(), nullptr, nullptr,
+                                  9, Hq, Hkv, D, eps, 0);
+      e = std::fmax(relerr(download<uint16_t>(ctx, tq2), q2), relerr(download<uint16_t>(ctx, tk2), k2));
+      expect(e <= 1e-2, "decode_prepare_qkv (rope_freq table used as given)", e);
+    }
     // prefill: head_rms_norm then apply_rope_partial with a text shift
     u16v xq = rand_bf16(size_t(S) * Hq * D), xk = rand_bf16(size_t(S) * Hkv * D);
     Tensor txq = upload(ctx, xq, {S, Hq * D}, DType::bf16), txk = upload(ctx, xk, {S, Hkv * D}, DType::bf16);
@@ -487,7 +509,7 @@ int main() {
     buf.attn_out = Tensor::allocate(ctx, {S, Hq * D});
     buf.scores = Tensor::allocate(ctx, {1}, DType::f32);
     buf.decode_scores = Tensor::allocate(ctx, {Hq, max_seq}, DType::f32);
-    buf.rope_freq = Tensor::allocate(ctx, {D / 2}, DType::f32);
+    buf.rope_freq = rope_freq_table(ctx, D, cfg.rope_theta);
     attention_layer(ctx, cfg, kv, buf, layer, 0, S, 0);
     u16v got_pre = download<uint16_t>(ctx, buf.attn_out);
     // oracle: norms, rope, cache, naive prefill

@@ -400,3 +400,43 @@ def test_fused_prepare_append_decode_mrope(apply_gate, split):
     kc_h = _np(kc_d)
     for b in range(B):
         _agree(kc_h[b, :, pos[b]], ko[b])
+
+
+def test_decode_prepare_with_a_frequency_table():
+    """ops::decode_prepare_qkv's rope_freq table (angle = start_pos *
+    rope_freq[d], ElementwiseOps.cpp:105-216) passed as rope_pos.inv_freq,
+    with a table that is not theta's (position-interpolated low
+    frequencies), in the decode prep and in the one-launch prep + decode."""
+    import torch
+    import aila_amd
+    Hq, Hkv, D, theta, eps, max_seq, pos = 16, 4, 128, 1e6, 1e-6, 2048, 1500
+    table = (1.0 / theta ** (np.arange(D // 2) * 2.0 / D)).astype(np.float32)
+    table[D // 4:] *= 0.125
+    q = dg.normal_bf16(1950, 0, (1, Hq, D), std=2.0)
+    k = dg.normal_bf16(1950, 1, (1, Hkv, D), std=2.0)
+    v = dg.normal_bf16(1950, 2, (1, Hkv, D))
+    qw = dg.normal_bf16(1950, 3, (D,))
+    kw = dg.normal_bf16(1950, 4, (D,))
+    dev = aila_amd.rope_pos(inv_freq=_t(table))
+    q_d, k_d = _t(q), _t(k)
+    aila_amd.decode_prepare_qkv(q_d, k_d, _t(v), _t(qw), _t(kw), pos=pos, rotary_dim=D, theta=theta, eps=eps,
+                                rope=dev)
+    torch.cuda.synchronize()
+    qo, ko = oracle.decode_prepare_qkv_freq(q[0], k[0], v[0], table, qw, kw, None, None, pos, Hq, Hkv, D, eps, 0)
+    _agree(_np(q_d)[0], qo)
+    _agree(_np(k_d)[0], ko)
+    # the fused launch with the same table
+    kc = dg.normal_bf16(1950, 5, (1, Hkv, max_seq, D))
+    vc = dg.normal_bf16(1950, 6, (1, Hkv, max_seq, D))
+    kc_d, vc_d = _t(kc), _t(vc)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(1, Hq, D), dtype=torch.uint8, device="cuda")
+    out = aila_amd.gqa_decode_prepare_append(_t(q), _t(k), _t(v), kc_d, vc_d, pos, q_norm_w=_t(qw), k_norm_w=_t(kw),
+                                             rotary_dim=D, theta=theta, eps=eps, workspace=ws, rope=dev)
+    torch.cuda.synchronize()
+    kc2, vc2 = kc.copy(), vc.copy()
+    qo2, _ = oracle.decode_prepare_qkv_freq(q[0], k[0], v[0], table, qw, kw, kc2[0], vc2[0], pos, Hq, Hkv, D, eps,
+                                            max_seq)
+    want = oracle.attention_decode_baseline(qo2[None], kc2, vc2, 1, Hq, Hkv, D, max_seq, pos + 1)
+    assert _relerr(_np(out), want) <= TOL
+    _agree(_np(kc_d)[0, :, pos], kc2[0, :, pos])
+

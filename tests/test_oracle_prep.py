@@ -126,3 +126,33 @@ def test_sigmoid_mul_closed_forms_and_numpy():
     want = dg.bf16_to_f32(x).astype(np.float64) / (1.0 + np.exp(-dg.bf16_to_f32(g).astype(np.float64)))
     got = dg.bf16_to_f32(oracle.sigmoid_mul(x, g)).astype(np.float64)
     assert np.max(np.abs(got - want)) <= 2 ** -8 * np.max(np.abs(want))
+
+
+def test_decode_prepare_with_the_backends_frequency_table():
+    """decode_prepare_qkv with rope_freq (ElementwiseOps.cpp:105-216): the
+    backends' own table 1/theta^(2d/D) (Qwen3DenseBackend.cpp:232-236) gives
+    the theta form bit for bit; an all-zero table rotates nothing (the
+    normalised heads); a table scaled by s at position p equals the theta
+    form at position s*p when s*p is an integer the float product keeps."""
+    Hq, Hkv, D, theta, eps = 8, 2, 128, 1e6, 1e-6
+    q = dg.normal_bf16(510, 0, (Hq, D))
+    k = dg.normal_bf16(510, 1, (Hkv, D))
+    v = dg.normal_bf16(510, 2, (Hkv, D))
+    qw = dg.normal_bf16(510, 3, (D,))
+    kw = dg.normal_bf16(510, 4, (D,))
+    table = np.array([np.float32(1.0) / np.power(np.float32(theta), np.float32(2.0 * d) / np.float32(D),
+                                                  dtype=np.float32) for d in range(D // 2)], np.float32)
+    # the oracle's theta form computes the same float table
+    qa, ka = oracle.decode_prepare_qkv_freq(q, k, v, table, qw, kw, None, None, 777, Hq, Hkv, D, eps, 0)
+    qb, _, kb = oracle.decode_prepare(q[None], k[None], v[None], qw, kw, None, None, np.array([777], np.int32), 1,
+                                      Hq, Hkv, D, 0, D, theta, eps)
+    assert np.array_equal(qa, qb[0]) and np.array_equal(ka, kb[0])
+    qz, kz = oracle.decode_prepare_qkv_freq(q, k, v, np.zeros(D // 2, np.float32), qw, kw, None, None, 777, Hq, Hkv,
+                                            D, eps, 0)
+    assert np.array_equal(qz.reshape(1, -1), oracle.head_rms_norm(q.reshape(1, -1), eps, 1, Hq, D, w_bf16=qw))
+    assert np.array_equal(kz.reshape(1, -1), oracle.head_rms_norm(k.reshape(1, -1), eps, 1, Hkv, D, w_bf16=kw))
+    qs, ks = oracle.decode_prepare_qkv_freq(q, k, v, table * np.float32(0.5), qw, kw, None, None, 1000, Hq, Hkv, D,
+                                            eps, 0)
+    qt, _, kt = oracle.decode_prepare(q[None], k[None], v[None], qw, kw, None, None, np.array([500], np.int32), 1,
+                                      Hq, Hkv, D, 0, D, theta, eps)
+    assert np.array_equal(qs, qt[0]) and np.array_equal(ks, kt[0])
