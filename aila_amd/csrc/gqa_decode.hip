@@ -376,6 +376,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   // compiler does not order that first LDS read after the DMA by itself: the
   // rotated loop of the fused-preparation kernel read the stage before it
   // landed (stale LDS from the previous workgroup).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
   int pg_nxt = page_of(t0 + kWaves * kChunk);
   for (int it = 0; t0 < s1; ++it, t0 += kWaves * kChunk) {
     const int stage = it & 1;

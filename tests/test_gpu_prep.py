@@ -440,3 +440,58 @@ def test_decode_prepare_with_a_frequency_table():
     assert _relerr(_np(out), want) <= TOL
     _agree(_np(kc_d)[0, :, pos], kc2[0, :, pos])
 
+
+def test_fused_decode_first_chunk_waits_for_its_dma():
+    """The wave whose first K chunk holds the appended row issues that
+    chunk's LDS DMA after the append, just before the loop that reads it; the
+    kernel waits for it explicitly (without the wait the G = 8 fused kernel
+    read the stage before it landed, now and then, and scored stale LDS).
+    Split 23 of 24 is that split here (1501 rows in 64-row splits). Every
+    split record is checked against float64 attention over its rows, on
+    repeated launches."""
+    import torch
+    import aila_amd
+    B, Hq, Hkv, D, rot = 2, 8, 1, 128, 32
+    seed, theta, eps, max_seq, p = 918, 1e7, 1e-6, 2048, 1500
+    pos = np.full(B, p, np.int32)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc0 = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
+    vc0 = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
+    kc, vc = kc0.copy(), vc0.copy()
+    qo, gw, _ = oracle.decode_prepare(q, k, v, qw, kw, kc, vc, pos, B, Hq, Hkv, D, max_seq, rot, theta, eps,
+                                      packed=True)
+    f64 = lambda x: dg.bf16_to_f32(x).astype(np.float64)
+    wsb = aila_amd.gqa_decode_workspace_size(B, Hq, D)
+    nmax = wsb // (B * Hq * (16 + D) * 4)
+    want_out = [oracle.attention_decode_baseline(qo[b:b + 1], kc[b:b + 1], vc[b:b + 1], 1, Hq, Hkv, D, max_seq,
+                                                 p + 1)[0] for b in range(B)]
+    for rep in range(24):
+        # fresh host uploads each launch: the cache rows are not in L2, so
+        # the K DMA is slow to land (the case the wait is for)
+        ws = torch.full((wsb // 4,), float("nan"), dtype=torch.float32, device="cuda")
+        out, _ = aila_amd.gqa_decode_prepare_append(_t(q), _t(k), _t(v), _t(kc0), _t(vc0), p, q_norm_w=_t(qw),
+                                                    k_norm_w=_t(kw), rotary_dim=rot, theta=theta, eps=eps,
+                                                    packed_gate=True, workspace=ws.view(torch.uint8))
+        torch.cuda.synchronize()
+        rec = ws.cpu().numpy().reshape(B, Hq, nmax, 16 + D)
+        ns = int(np.sum(np.isfinite(rec[0, 0, :, 1])))
+        assert ns == 24, ns
+        got = _np(out)
+        for b in range(B):
+            assert _relerr(got[b], want_out[b]) <= TOL, f"launch {rep} sequence {b}"
+            Kb, Vb = f64(kc[b, 0, :p + 1]), f64(vc[b, 0, :p + 1])
+            S = f64(qo[b]) @ Kb.T / np.sqrt(D)
+            for i in range(ns):
+                s0, s1 = 64 * i, min(64 * i + 64, p + 1)
+                m = S[:, s0:s1].max(axis=1, keepdims=True)
+                w = np.exp(S[:, s0:s1] - m)
+                want = (w @ Vb[s0:s1]) / w.sum(axis=1, keepdims=True)
+                r = rec[b, :, i].astype(np.float64)
+                np.testing.assert_allclose(r[:, 0], m[:, 0], rtol=1e-3, atol=1e-3,
+                                           err_msg=f"launch {rep} sequence {b} split {i} max")
+                err = np.abs(r[:, 16:] / r[:, 1:2] - want).max() / np.abs(want).max()
+                assert err <= 2e-2, f"launch {rep} sequence {b} split {i}: {err}"
