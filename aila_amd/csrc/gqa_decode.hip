@@ -781,9 +781,18 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
   if (workspace && a.nsplit_max < 2)
     return set_error(AILA_HIP_EWORKSPACE, "gqa_decode: workspace %zu bytes holds < 2 split records (%zu bytes each)",
                      workspace_bytes, rec_bytes);
+  // Short contexts run single-pass even with a workspace: up to two 16-row
+  // chunks per wave (128 rows; 256 at D <= 128, where a chunk costs less)
+  // one launch beats split + merge (graph replay, B=1 Hq=16 Hkv=8 D=128:
+  // 4.2 against 6.5 us at 128 rows, 5.6 against 6.6 at 256; D=256 Hkv=4:
+  // 7.1 against 8.3 at 128 rows, the split ahead from 192).
+  const int single_max = D <= 128 ? 4 * kWaves * kChunk : 2 * kWaves * kChunk;
   if (plan_len == 0) {
     // Nothing to attend: the single-pass kernel writes a zero output.
     a.split_len = 1;
+    a.nsplit = 1;
+  } else if (workspace && plan_len <= single_max) {
+    a.split_len = plan_len;
     a.nsplit = 1;
   } else if (workspace) {
     // One round of resident workgroups; splits are multiples of 64 rows
