@@ -9,7 +9,12 @@ not pin one by one, each case checked against the CPU oracle:
   - the fused decode preparation + append + decode at device positions;
   - the whole DeltaNet layer, prefill then decode steps.
 Attention outputs within max relative error 1e-2, DeltaNet states within
-1e-3; cache rows and pool pages past the attended range hold NaN."""
+1e-3; cache rows and pool pages past the attended range hold NaN.
+
+AILA_SWEEP_SEED=n draws another set of cases (default 0: the set the suite
+runs by default)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -18,6 +23,7 @@ from aila_amd import datagen as dg
 
 pytestmark = pytest.mark.gpu
 ATTN_TOL = 1e-2
+SWEEP_SEED = int(os.environ.get("AILA_SWEEP_SEED", "0"))
 
 
 def _t(x):
@@ -37,7 +43,7 @@ def _relerr(a, r):
 
 
 def _decode_cases():
-    rng = np.random.default_rng(0x5EE9)
+    rng = np.random.default_rng(0x5EE9 + SWEEP_SEED)
     cases = []
     for i in range(16):
         D = int(rng.choice([64, 128, 256]))
@@ -78,7 +84,7 @@ def test_sweep_decode_device_lengths(i, D, G, Hkv, B, bound, lens):
 
 
 def _prefill_cases():
-    rng = np.random.default_rng(0x5EEA)
+    rng = np.random.default_rng(0x5EEA + SWEEP_SEED)
     cases = []
     for i in range(16):
         D = int(rng.choice([64, 128, 256]))
@@ -115,7 +121,7 @@ def test_sweep_prefill_cached(i, D, G, Hkv, S, start):
 
 
 def _prefill_uncached_cases():
-    rng = np.random.default_rng(0x5EEB)
+    rng = np.random.default_rng(0x5EEB + SWEEP_SEED)
     cases = []
     for i in range(12):
         D = int(rng.choice([64, 128, 256]))
@@ -156,7 +162,7 @@ def test_sweep_prefill_with_cache_write(i, D, G, Hkv, S, cache_pos):
 
 
 def _deltanet_prefill_cases():
-    rng = np.random.default_rng(0x5EEC)
+    rng = np.random.default_rng(0x5EEC + SWEEP_SEED)
     cases = []
     for i in range(12):
         B = int(rng.integers(1, 4))
@@ -199,7 +205,7 @@ def test_sweep_deltanet_prefill(i, B, T, Hk, Hv, gates, s0):
 
 
 def _deltanet_decode_cases():
-    rng = np.random.default_rng(0x5EED)
+    rng = np.random.default_rng(0x5EED + SWEEP_SEED)
     cases = []
     for i in range(12):
         dk = int(rng.choice([64, 128, 256]))
@@ -238,7 +244,7 @@ def test_sweep_deltanet_decode(i, B, Hk, Hv, dk, dv):
 
 
 def _paged_cases():
-    rng = np.random.default_rng(0x5EEE)
+    rng = np.random.default_rng(0x5EEE + SWEEP_SEED)
     cases = []
     for i in range(12):
         page = int(rng.choice([16, 32, 48, 64, 128, 256]))
@@ -294,7 +300,7 @@ def test_sweep_paged_decode(i, page, D, G, B, max_pages, lens):
 
 
 def _fused_prep_cases():
-    rng = np.random.default_rng(0x5EEF)
+    rng = np.random.default_rng(0x5EEF + SWEEP_SEED)
     cases = []
     for i in range(10):
         D = int(rng.choice([64, 128, 256]))
@@ -352,7 +358,7 @@ def test_sweep_fused_prepare_append_decode(i, D, G, Hkv, B, rot, packed, split, 
 
 
 def _layer_cases():
-    rng = np.random.default_rng(0x5EF1)
+    rng = np.random.default_rng(0x5EF1 + SWEEP_SEED)
     cases = []
     for i in range(8):
         B = int(rng.integers(1, 4))
@@ -412,7 +418,7 @@ def test_sweep_layer_prefill_then_decode(i, B, Hk, Hv, T, steps, head0, wide):
 
 
 def _append_cases():
-    rng = np.random.default_rng(0x5EF2)
+    rng = np.random.default_rng(0x5EF2 + SWEEP_SEED)
     cases = []
     for i in range(10):
         D = int(rng.choice([64, 128, 256]))
