@@ -69,6 +69,104 @@ def deltanet_layer_bytes(B, Hk, Hv, d):
             + B * Hv * d * 2 + ch * 4 * 2)
 
 
+def _drm_device_dir(torch):
+    """sysfs directory of the DRM card that is torch device 0 (matched by
+    PCI address), or None."""
+    import glob
+    try:
+        pr = torch.cuda.get_device_properties(0)
+        want = f"{pr.pci_domain_id:04x}:{pr.pci_bus_id:02x}:{pr.pci_device_id:02x}"
+    except Exception:
+        want = None
+    cards = sorted(glob.glob("/sys/class/drm/card[0-9]*/device/pp_dpm_sclk"))
+    for c in cards:
+        d = os.path.dirname(c)
+        if want and os.path.basename(os.path.realpath(d)).startswith(want):
+            return d
+    return os.path.dirname(cards[0]) if len(cards) == 1 else None
+
+
+def _dpm_levels(path):
+    """(MHz of every level, MHz of the current '*' level) of a pp_dpm file."""
+    levels, cur = [], None
+    for line in open(path).read().splitlines():
+        f = line.split()
+        if len(f) < 2 or not f[1].lower().endswith("mhz"):
+            continue
+        mhz = int(float(f[1][:-3]))
+        if not f[0].startswith("S"):
+            levels.append(mhz)
+        if line.rstrip().endswith("*"):
+            cur = mhz
+    return levels, cur
+
+
+class ClockSampler:
+    """Samples the shader clock (the current pp_dpm_sclk level, which reads
+    the actual frequency under load) and board power (hwmon power1_input)
+    every ~5 ms from a host thread while active; sysfs reads only, so the
+    GPU work is untouched."""
+
+    def __init__(self, torch):
+        import threading
+        self.dev = _drm_device_dir(torch)
+        self.sclk, self.power = [], []
+        self._stop = threading.Event()
+        self._t = None
+
+    def _run(self):
+        import glob
+        pw = sorted(glob.glob(os.path.join(self.dev, "hwmon", "hwmon*", "power1_input")))
+        while not self._stop.is_set():
+            try:
+                _, cur = _dpm_levels(os.path.join(self.dev, "pp_dpm_sclk"))
+                if cur is not None:
+                    self.sclk.append(cur)
+                if pw:
+                    self.power.append(int(open(pw[0]).read()) / 1e6)
+            except Exception:
+                pass
+            self._stop.wait(0.005)
+
+    def __enter__(self):
+        import threading
+        if self.dev:
+            self._t = threading.Thread(target=self._run, daemon=True)
+            self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._t:
+            self._t.join()
+
+    def summary(self):
+        if not self.sclk:
+            return None
+        out = {"sclk_mhz": {"min": min(self.sclk), "median": statistics.median(self.sclk), "max": max(self.sclk),
+                            "samples": len(self.sclk)}}
+        if self.power:
+            out["board_power_w"] = {"median": round(statistics.median(self.power), 1),
+                                    "max": round(max(self.power), 1)}
+        return out
+
+
+def device_info(torch):
+    """GPU identity and clock levels (sysfs pp_dpm tables), for the record."""
+    pr = torch.cuda.get_device_properties(0)
+    info = {"name": pr.name, "arch": pr.gcnArchName, "compute_units": pr.multi_processor_count,
+            "memory_gib": round(pr.total_memory / 2 ** 30, 1)}
+    d = _drm_device_dir(torch)
+    try:
+        if d:
+            info["sclk_levels_mhz"] = _dpm_levels(os.path.join(d, "pp_dpm_sclk"))[0]
+            mlev, mcur = _dpm_levels(os.path.join(d, "pp_dpm_mclk"))
+            info["mclk_mhz"] = mcur if mcur is not None else (max(mlev) if mlev else None)
+    except Exception:
+        pass
+    return info
+
+
 def time_graph(torch, g, reps):
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -141,7 +239,7 @@ def step5(aila_amd, W, p):
     W["positions"].add_(1)
 
 
-def bench_config5(torch, aila_amd, steps, warmup):
+def bench_config5(torch, aila_amd, steps, warmup, sampler=None):
     W = build_config5(torch, aila_amd, steps, warmup)
     graphs = []
     # capture NPOOL graphs, one per activation set; capture does not execute,
@@ -165,13 +263,15 @@ def bench_config5(torch, aila_amd, steps, warmup):
     L_first = int(W["positions"][0].item()) + 1
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    s.record()
-    for i in range(steps):
-        graphs[(warmup + i) % NPOOL].replay()
-    e.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    import contextlib
+    with sampler if sampler is not None else contextlib.nullcontext():
+        t0 = time.perf_counter()
+        s.record()
+        for i in range(steps):
+            graphs[(warmup + i) % NPOOL].replay()
+        e.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ms = s.elapsed_time(e) / steps
     # algorithmic bytes per step, averaged over the timed lengths
     L_mean = L_first + (steps - 1) / 2.0
@@ -1002,7 +1102,11 @@ def main():
             log(f"[profile] {args.profile_kernel}: {json.dumps(r)}")
         return
     log(f"[bench] config 5: {args.warmup} warmup + {args.steps} timed steps")
-    r5 = bench_config5(torch, aila_amd, args.steps, args.warmup)
+    device = device_info(torch)
+    clocks = ClockSampler(torch)
+    r5 = bench_config5(torch, aila_amd, args.steps, args.warmup, sampler=clocks)
+    device["during_timed_steps"] = clocks.summary()
+    log(f"[bench] device {device}")
     value = r5["step_bytes"] / (r5["ms"] * 1e-3) / 1e9
     log(f"[bench] config 5: {r5['ms']:.3f} ms/step, {value:.0f} GB/s")
     roof = roofline_gqa(torch, aila_amd, r5["W"])
@@ -1064,6 +1168,7 @@ def main():
         },
         "roofline": roof,
         "cpu_baseline": cpu,
+        "device": device,
         "sub": sub,
     }
     print(json.dumps(line), flush=True)
