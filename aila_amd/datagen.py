@@ -10,7 +10,7 @@ The generator is counter based so any host (and the GPU fill kernel in
   * Box-Muller in fp64: ``r = sqrt(-2 ln u1)``, ``z0 = r cos(2 pi u2)``,
     ``z1 = r sin(2 pi u2)``; values are rounded to fp32.
 
-Seeds follow the survey's convention ``0xA11A + config_index``; each tensor of
+Seeds are ``0xA11A + config_index`` for the benchmark configs; each tensor of
 a config draws its own stream index in a fixed order.
 """
 from __future__ import annotations
