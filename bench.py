@@ -87,18 +87,23 @@ def _drm_device_dir(torch):
 
 
 def _dpm_levels(path):
-    """(MHz of every level, MHz of the current '*' level) of a pp_dpm file."""
+    """(MHz of the table's fixed levels, MHz of the current '*' line) of a
+    pp_dpm file. The current line reads the actual clock: between levels
+    the driver shows it as an extra starred entry, so starred entries are
+    left out of the levels (a table with only a starred entry keeps it)."""
     levels, cur = [], None
     for line in open(path).read().splitlines():
         f = line.split()
         if len(f) < 2 or not f[1].lower().endswith("mhz"):
             continue
         mhz = int(float(f[1][:-3]))
-        if not f[0].startswith("S"):
-            levels.append(mhz)
         if line.rstrip().endswith("*"):
             cur = mhz
-    return levels, cur
+        elif not f[0].startswith("S"):
+            levels.append(mhz)
+    if not levels and cur is not None:
+        levels = [cur]
+    return sorted(levels), cur
 
 
 class ClockSampler:
