@@ -2,7 +2,10 @@
 
 Every source under ``aila_amd/csrc`` (``*.hip`` device code, ``*.cpp`` host
 code) is compiled by hipcc for gfx950 into ``aila_amd/_build`` and linked
-into one shared library. Run ``python -m aila_amd.build``.
+into one shared library. The C++ ``ops::`` layer (``aila_amd/host``) links
+against it as ``libaila_ops.so``; ``aila_amd/probe`` builds the benchmark's
+streaming-read probe into ``libaila_probe.so``, which the product never
+loads. Run ``python -m aila_amd.build``.
 
 HIP code is compiled with packed-FP32 instruction selection disabled
 (``-packed-fp32-ops``); hipcc's host pass warns that it does not know that
@@ -22,6 +25,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libaila_hip.so")
 OPS_LIB = os.path.join(HERE, "libaila_ops.so")
+PROBE_LIB = os.path.join(HERE, "libaila_probe.so")
 HOST = os.path.join(HERE, "host")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -67,8 +71,13 @@ def build(verbose: bool = False) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"ops layer build failed:\n{r.stderr}")
+    # measurement probe for the benchmark (not part of the product library)
+    cmd = [HIPCC, *COMMON, "-shared", os.path.join(HERE, "probe", "stream_read.hip"), "-o", PROBE_LIB]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe build failed:\n{r.stderr}")
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources and {OPS_LIB}")
+        print(f"built {LIB} from {len(srcs)} sources, {OPS_LIB} and {PROBE_LIB}")
     return LIB
 
 

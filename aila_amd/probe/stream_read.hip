@@ -1,0 +1,65 @@
+// Streaming-read probe: the HBM read rate this chip reaches over the GQA
+// decode's exact K/V layout, reported beside the decode's roofline as the
+// achievable ceiling. Measurement only: it is built into its own library
+// (libaila_probe.so), which the benchmark loads and the product never does.
+//
+// Grid (split, kv head, sequence), 256 threads, as the decode's split
+// kernel: workgroup (s, h, b) reads rows [s*len/nsplit, (s+1)*len/nsplit)
+// of K[b, h] and of V[b, h] (cache [B, Hkv, max_seq, D] bf16) once, with
+// 16-byte nontemporal loads, sixteen in flight per thread, and folds them
+// into a value that is stored only if it equals a constant no input
+// produces in practice (so the loads cannot be dropped).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kThreads = 256;
+constexpr int kUnroll = 16;
+
+__global__ __launch_bounds__(kThreads) void stream_read_kernel(const unsigned char* __restrict__ k,
+                                                               const unsigned char* __restrict__ v, int Hkv,
+                                                               long max_seq, long len, int D, unsigned* sink) {
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const long rows = (len + gridDim.x - 1) / gridDim.x;
+  const long r0 = split * rows, r1 = r0 + rows < len ? r0 + rows : len;
+  if (r0 >= r1) return;
+  const size_t row_bytes = static_cast<size_t>(D) * 2;
+  const size_t base = ((static_cast<size_t>(b) * Hkv + h) * max_seq + r0) * row_bytes;
+  const size_t n16 = (r1 - r0) * row_bytes / 16;
+  uint32_t acc = 0;
+  for (int t = 0; t < 2; ++t) {
+    const u32x4* p = reinterpret_cast<const u32x4*>((t == 0 ? k : v) + base);
+    size_t i = threadIdx.x;
+    for (; i + (kUnroll - 1) * kThreads < n16; i += kUnroll * kThreads) {
+      u32x4 x[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) x[u] = __builtin_nontemporal_load(p + i + u * kThreads);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc ^= x[u][0] ^ x[u][1] ^ x[u][2] ^ x[u][3];
+    }
+    for (; i < n16; i += kThreads) {
+      const u32x4 x = __builtin_nontemporal_load(p + i);
+      acc ^= x[0] ^ x[1] ^ x[2] ^ x[3];
+    }
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+}  // namespace
+
+// Reads rows [0, len) of every (sequence, kv head) of k_cache and v_cache
+// ([B, Hkv, max_seq, D] bf16) once, in nsplit workgroups per (sequence, kv
+// head). sink: one device unsigned. Returns a hipError_t.
+extern "C" int aila_probe_stream_read(const void* k_cache, const void* v_cache, int B, int Hkv, long max_seq,
+                                      long len, int D, int nsplit, unsigned* sink, void* stream) {
+  if (!k_cache || !v_cache || !sink || B <= 0 || B > 65535 || Hkv <= 0 || Hkv > 65535 || nsplit <= 0 ||
+      len <= 0 || len > max_seq || D <= 0 || (D * 2) % 16 != 0)
+    return static_cast<int>(hipErrorInvalidValue);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(nsplit, Hkv, B), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const unsigned char*>(k_cache),
+                     static_cast<const unsigned char*>(v_cache), Hkv, max_seq, len, D, sink);
+  return static_cast<int>(hipGetLastError());
+}

@@ -426,10 +426,55 @@ def roofline_gqa(torch, aila_amd, W, reps=64):
             note = "rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel source, calibrated on a 1 GiB copy"
         else:
             note = "counter profile is stale (kernel source changed since it was measured)"
-    return {"kernel": "gqa_decode_split_kernel<256,4> + merge", "bound": "hbm",
-            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": note,
-            "algorithmic_bytes": byts, "avg_launch_us": round(avg_ms * 1e3, 2)}
+    out = {"kernel": "gqa_decode_split_kernel<256,4> + merge", "bound": "hbm",
+           "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": note,
+           "algorithmic_bytes": byts, "avg_launch_us": round(avg_ms * 1e3, 2)}
+    ach = achievable_read(torch, W["kc"][0], W["vc"][0], L, reps)
+    if ach is not None:
+        out["achievable"] = dict(ach, frac_of_achievable=round(achieved / ach["read_gbs"], 4))
+    return out
+
+
+def achievable_read(torch, kc, vc, L, reps):
+    """The streaming-read probe (aila_amd/libaila_probe.so) over the same
+    K/V rows the decode launch reads, in as many workgroups (one round of
+    resident workgroups: 16 splits per sequence and KV head at config 5),
+    timed like the decode. None if the probe library is absent."""
+    import ctypes
+    path = os.path.join(ROOT, "aila_amd", "libaila_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.aila_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_long, ctypes.c_long, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.c_void_p]
+    lib.aila_probe_stream_read.restype = ctypes.c_int
+    B, Hkv, max_seq, D = kc.shape
+    nsplit = max(1, 512 // (B * Hkv))
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fn():
+        rc = lib.aila_probe_stream_read(kc.data_ptr(), vc.data_ptr(), B, Hkv, max_seq, L, D, nsplit,
+                                        sink.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"aila_probe_stream_read: hipError {rc}")
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.4e9 * 0.02))
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    avg_ms = s.elapsed_time(e) / reps
+    byts = 2 * B * Hkv * L * D * 2
+    return {"read_gbs": round(byts / (avg_ms * 1e-3) / 1e9, 1), "read_bytes": byts,
+            "avg_launch_us": round(avg_ms * 1e3, 2),
+            "probe": f"streaming read of the same K/V rows, {nsplit * Hkv * B} workgroups, 16-byte nontemporal loads"}
 
 
 def decode_source_stamp():
