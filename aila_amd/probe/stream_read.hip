@@ -1,8 +1,11 @@
-// Streaming-read probe: the HBM read rate this chip reaches over the GQA
-// decode's exact K/V layout, reported beside the decode's roofline as the
-// achievable ceiling. Measurement only: it is built into its own library
-// (libaila_probe.so), which the benchmark loads and the product never does.
+// Ceiling probes for the benchmark: the HBM read rate this chip reaches
+// over the GQA decode's exact K/V layout, and the dense bf16 MFMA rate it
+// sustains, reported beside the decode's and the prefill's rooflines as the
+// achievable ceilings. Measurement only: they are built into their own
+// library (libaila_probe.so), which the benchmark loads and the product
+// never does.
 //
+// Streaming read:
 // Grid (split, kv head, sequence), 256 threads, as the decode's split
 // kernel: workgroup (s, h, b) reads rows [s*len/nsplit, (s+1)*len/nsplit)
 // of K[b, h] and of V[b, h] (cache [B, Hkv, max_seq, D] bf16) once, with
@@ -16,6 +19,8 @@
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kThreads = 256;
 constexpr int kUnroll = 16;
 
@@ -48,6 +53,32 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const unsigned ch
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// Dense MFMA: every wave issues `iters` rounds of 16 independent
+// v_mfma_f32_16x16x32_bf16 (16,384 FLOP each) on register operands; the
+// accumulators are folded and stored only if they equal a constant no run
+// produces, so nothing is dropped. Two waves per SIMD, as the prefill runs.
+constexpr int kAcc = 16;
+__global__ __launch_bounds__(kThreads) void mfma_kernel(int iters, float seed, float* sink) {
+  const float x = seed + static_cast<float>(threadIdx.x & 7) * 0.001f;
+  bf16x8 a, b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = static_cast<__bf16>(x + e * 0.01f);
+    b[e] = static_cast<__bf16>(x - e * 0.01f);
+  }
+  f32x4 c[kAcc];
+#pragma unroll
+  for (int j = 0; j < kAcc; ++j) c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < kAcc; ++j) c[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c[j], 0, 0, 0);
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int j = 0; j < kAcc; ++j) t += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+  if (t == 1234.5f) sink[0] = t;
+}
+
 }  // namespace
 
 // Reads rows [0, len) of every (sequence, kv head) of k_cache and v_cache
@@ -61,5 +92,15 @@ extern "C" int aila_probe_stream_read(const void* k_cache, const void* v_cache, 
   hipLaunchKernelGGL(stream_read_kernel, dim3(nsplit, Hkv, B), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const unsigned char*>(k_cache),
                      static_cast<const unsigned char*>(v_cache), Hkv, max_seq, len, D, sink);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Runs `blocks` workgroups of 256 threads (four waves), each wave issuing
+// iters * 16 dense 16x16x32 bf16 MFMAs; FLOPs = blocks * 4 * iters * 16 *
+// 16384. sink: one device float. Returns a hipError_t.
+extern "C" int aila_probe_mfma(int blocks, int iters, float* sink, void* stream) {
+  if (!sink || blocks <= 0 || iters <= 0) return static_cast<int>(hipErrorInvalidValue);
+  hipLaunchKernelGGL(mfma_kernel, dim3(blocks), dim3(kThreads), 0, static_cast<hipStream_t>(stream), iters, 0.5f,
+                     sink);
   return static_cast<int>(hipGetLastError());
 }

@@ -172,6 +172,18 @@ def device_info(torch):
     return info
 
 
+def steady(torch, fn, ms=60.0):
+    """Calls fn back to back for about `ms` of wall time so the timing that
+    follows sees the steady-state shader clock: from idle the clock takes
+    tens of milliseconds to ramp (the config-2 prefill measures 52-54 us
+    cold, 45 us after 50 ms of calls)."""
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_graph(torch, g, reps):
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -557,7 +569,7 @@ def profile_kernel(torch, aila_amd, reps=20):
 
 
 # ------------------------------------------------------------ sub-metrics --
-def sub_prefill(torch, aila_amd, reps=20):
+def sub_prefill(torch, aila_amd, reps=100):
     S, Hq, Hkv, D = 2048, 32, 8, 128
     g = torch.Generator(device="cuda")
     g.manual_seed(0xA11A + 1)
@@ -574,8 +586,7 @@ def sub_prefill(torch, aila_amd, reps=20):
     kc = torch.empty((Hkv, S, D), **bf)
     vc = torch.empty_like(kc)
     fn = lambda: aila_amd.gqa_prefill(q, k, v, Hq, Hkv, out=out, k_cache=kc, v_cache=vc)
-    for _ in range(3):
-        fn()
+    steady(torch, fn)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     s.record()
@@ -585,8 +596,43 @@ def sub_prefill(torch, aila_amd, reps=20):
     torch.cuda.synchronize()
     us = s.elapsed_time(e) / reps * 1e3
     flops = 4 * D * Hq * S * (S + 1) / 2
-    return {"config": "2: S=2048 Hq=32 Hkv=8 D=128 causal (QK-normed, RoPE'd inputs) + cache write", "us": round(us, 2),
-            "tflops": round(flops / us / 1e6, 1), "frac_of_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    res = {"config": "2: S=2048 Hq=32 Hkv=8 D=128 causal (QK-normed, RoPE'd inputs) + cache write", "us": round(us, 2),
+           "tflops": round(flops / us / 1e6, 1), "frac_of_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    ach = achievable_mfma(torch)
+    if ach is not None:
+        res["achievable_mfma_tflops"] = ach
+        res["frac_of_achievable"] = round(flops / us / 1e6 / ach, 4)
+    return res
+
+
+def achievable_mfma(torch, blocks=1024, iters=8192):
+    """Dense bf16 MFMA rate the chip sustains (aila_amd/libaila_probe.so:
+    independent v_mfma_f32_16x16x32_bf16 streams on every SIMD), TFLOP/s,
+    or None if the probe library is absent."""
+    import ctypes
+    path = os.path.join(ROOT, "aila_amd", "libaila_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.aila_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.aila_probe_mfma.restype = ctypes.c_int
+    sink = torch.zeros(1, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fn():
+        rc = lib.aila_probe_mfma(blocks, iters, sink.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"aila_probe_mfma: hipError {rc}")
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(3):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    sec = s.elapsed_time(e) / 3 * 1e-3
+    return round(blocks * 4 * iters * 16 * 16384 / sec / 1e12, 1)
 
 
 def sub_prefill_cached(torch, aila_amd, reps=20):
@@ -610,9 +656,7 @@ def sub_prefill_cached(torch, aila_amd, reps=20):
 
     def timed(fn):
         # HIP-graph replay of `reps` calls: the kernels' time, not the host's
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
+        steady(torch, fn)
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
             for _ in range(reps):
@@ -757,7 +801,7 @@ def sub_deltanet_layer_decode(torch, aila_amd, steps=512, per_graph=16):
             "state_evicted_note": "24 states in rotation, one per DeltaNet layer of the config-5 stack"}
 
 
-def sub_deltanet_prefill(torch, aila_amd, reps=10):
+def sub_deltanet_prefill(torch, aila_amd, reps=40):
     B, T, Hk, Hv, d = 1, 4096, 16, 32, 128
     g = torch.Generator(device="cuda")
     g.manual_seed(0xA11A + 3)
@@ -771,7 +815,7 @@ def sub_deltanet_prefill(torch, aila_amd, reps=10):
     out = torch.empty((B, T, Hv, d), **bf)
     ws = torch.empty(aila_amd.deltanet_prefill_workspace_size(B, T, Hv, d, d), dtype=torch.uint8, device="cuda")
     fn = lambda: aila_amd.deltanet_prefill(q, k, v, a, b, st, out=out, workspace=ws)
-    fn()
+    steady(torch, fn)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     s.record()
@@ -876,7 +920,7 @@ def sub_decode_prep(torch, aila_amd, per_graph=32, reps=20):
             "us_per_call": round(us, 2), "GBps": round(byts / us / 1e3, 1)}
 
 
-def sub_deltanet_layer_prefill(torch, aila_amd, reps=10):
+def sub_deltanet_layer_prefill(torch, aila_amd, reps=40):
     """Full layer prefill (conv ring + SiLU into hi/lo planes, chunked
     recurrence with the key/value residuals, RMSNorm*SiLU(z) gate) at the
     config-4 shape, from the backend's fused [qkv | z | a | b] rows."""
@@ -895,7 +939,7 @@ def sub_deltanet_layer_prefill(torch, aila_amd, reps=10):
     fn = lambda: aila_amd.deltanet_layer_prefill(fused[..., :ch], fused[..., ch:ch + zd],
                                                  fused[..., ch + zd:ch + zd + Hv], fused[..., ch + zd + Hv:], w, cs, 0,
                                                  nw, st, Hk, out=out, workspace=ws)
-    fn()
+    steady(torch, fn)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     s.record()
