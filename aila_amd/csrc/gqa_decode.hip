@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ kc,
     const bf16* __restrict__ vc, bf16* __restrict__ out,
     float* __restrict__ part, int Hq, int Hkv, int max_seq, int L,
-    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max,
+    const int* __restrict__ seq_lens, int len_bias, int split_len, int nsplit_max, int group,
     float scale_log2, const bf16* __restrict__ k_new, const bf16* __restrict__ v_new, PrepArgs pa, PageArgs pg,
     WinArgs wn) {
   static_assert(D % 32 == 0 && D <= 256, "D");
@@ -136,7 +136,15 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   constexpr int STAGE = kChunk * D * 2;          // bytes of one K stage (16 rows)
   constexpr int NDMA = STAGE / 1024;             // DMA instructions per stage per wave
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // Group of `group` = Hq/Hkv query heads per KV head, served G (the tile)
+  // at a time: grid.y = Hkv * chunks, and the workgroup of chunk c of KV
+  // head kvh holds query heads group*kvh + G*c .. + gv - 1 (gv <= G; rows of
+  // the tile past gv are zero and their results unused).
+  const int chunks = (group + G - 1) / G;
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int kvh = static_cast<int>(blockIdx.y) / chunks;
+  const int chunk = static_cast<int>(blockIdx.y) - kvh * chunks;
+  const int gv = min(G, group - chunk * G);
   int len = L;
   if (seq_lens) len = min(max(seq_lens[b] + len_bias, 0), L);
   // window: logical row t reads cache row t (t < wsink) or t + wgap
@@ -161,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   const size_t kv_off = PAGED ? 0 : (static_cast<size_t>(b) * Hkv + kvh) * max_seq * D;
   const bf16* K = kc + kv_off;
   const bf16* V = vc + kv_off;
-  const int h0 = kvh * G;             // first query head of the group
+  const int h0 = kvh * group + chunk * G;   // first query head of this workgroup
   // Element offset (from K / V) of cache row t0, the first row of a 16-row
   // chunk; rows t0 .. t0 + 15 follow it contiguously in both layouts.
   // `page` is the page holding t0 (paged layout only).
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 raw = {0u, 0u, 0u, 0u};
-      if (m16 < G) raw = ld16(q + (static_cast<size_t>(b) * Hq + h0 + m16) * D + ks * 32 + g4 * 8);
+      if (m16 < gv) raw = ld16(q + (static_cast<size_t>(b) * Hq + h0 + m16) * D + ks * 32 + g4 * 8);
       qa[ks] = as_bf16x8(raw);
     }
   } else {
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     }
     constexpr int E = D / 64;
 #pragma unroll
-    for (int hh = wave; hh < G; hh += kWaves) {
+    for (int hh = wave; hh < gv; hh += kWaves) {
       const bf16* qr = q + (static_cast<size_t>(b) * Hq + h0 + hh) * pa.q_stride;
       float xv[E], ss = 0.f;
 #pragma unroll
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
           pa.gate_out[(static_cast<size_t>(b) * Hq + h0 + hh) * D + d] = qr[D + d];
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * half; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < gv * half; idx += kThreads) {
       const int hh = idx / half, j = idx % half;
       const float x0 = s_q[hh][j], x1 = s_q[hh][j + half];
       const float c = s_tab[2 * j], sn = s_tab[2 * j + 1];
@@ -290,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 w = {0u, 0u, 0u, 0u};
-      if (m16 < G) {
+      if (m16 < gv) {
         const float* r = &s_q[m16][ks * 32 + g4 * 8];
         w = u32x4{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
                   pack_bf16x2(r[6], r[7])};
@@ -512,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
   __syncthreads();
 
   // ---- workgroup merge ------------------------------------------------
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < gv * D; idx += kThreads) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
@@ -653,6 +661,7 @@ struct DecodeArgs {
   const int* seq_lens;
   int len_bias;          // sequence b attends min(seq_lens[b] + len_bias, L) rows
   int split_len, nsplit, nsplit_max;
+  int group, chunks;     // Hq / Hkv, and workgroups per KV head (group / tile, rounded up)
   const bf16* k_new;     // fused append (null: none)
   const bf16* v_new;
   PrepArgs prep;         // q_stride = 0: no fused preparation
@@ -665,22 +674,22 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
   const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
   const bool win = a.win.window > 0;
   if (a.prep.q_stride > 0)
-    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, true>), dim3(a.nsplit, a.Hkv * a.chunks, a.B), dim3(kThreads), 0, st,
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
+                       a.split_len, a.nsplit_max, a.group, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
   else if (a.pages.table != nullptr)
-    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, true>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0,
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, true>), dim3(a.nsplit, a.Hkv * a.chunks, a.B), dim3(kThreads), 0,
                        st, a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
+                       a.split_len, a.nsplit_max, a.group, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
   else if (win)
-    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, false, true>), dim3(a.nsplit, a.Hkv, a.B),
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G, false, false, true>), dim3(a.nsplit, a.Hkv * a.chunks, a.B),
                        dim3(kThreads), 0, st, a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L,
-                       a.seq_lens, a.len_bias, a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep,
+                       a.seq_lens, a.len_bias, a.split_len, a.nsplit_max, a.group, scale_log2, a.k_new, a.v_new, a.prep,
                        a.pages, a.win);
   else
-    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv, a.B), dim3(kThreads), 0, st,
+    hipLaunchKernelGGL((gqa_decode_split_kernel<D, G>), dim3(a.nsplit, a.Hkv * a.chunks, a.B), dim3(kThreads), 0, st,
                        a.q, a.kc, a.vc, a.out, a.part, a.Hq, a.Hkv, a.max_seq, a.L, a.seq_lens, a.len_bias,
-                       a.split_len, a.nsplit_max, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
+                       a.split_len, a.nsplit_max, a.group, scale_log2, a.k_new, a.v_new, a.prep, a.pages, a.win);
   if (a.part) {
     const bool gated = a.prep.q_stride > 0 && a.prep.apply_gate;
     if (win)
@@ -693,6 +702,11 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
   }
   return check_launch("gqa_decode");
 }
+
+// Query-head tile of the split kernel for a group of g query heads per KV
+// head: the smallest of 1, 2, 4, 8 that holds it, else 8 (several
+// workgroups per KV head, each streaming its K/V; see the kernel).
+int decode_tile(int g) { return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : 8; }
 
 // Workgroups of the split kernel that the device holds at once (occupancy x
 // CUs), per device, computed on first use. The split count targets exactly
@@ -720,7 +734,7 @@ int resident_workgroups() {
 int resident_for(int D, int G) {
   auto pick = [&](auto d_tag) -> int {
     constexpr int DD = decltype(d_tag)::value;
-    switch (G) {
+    switch (decode_tile(G)) {
       case 1: return resident_workgroups<DD, 1>();
       case 2: return resident_workgroups<DD, 2>();
       case 4: return resident_workgroups<DD, 4>();
@@ -737,13 +751,12 @@ int resident_for(int D, int G) {
 }
 
 template <int D>
-int dispatch_g(int G, const DecodeArgs& a, hipStream_t st) {
-  switch (G) {
+int dispatch_g(const DecodeArgs& a, hipStream_t st) {
+  switch (decode_tile(a.group)) {
     case 1: return launch_decode<D, 1>(a, st);
     case 2: return launch_decode<D, 2>(a, st);
     case 4: return launch_decode<D, 4>(a, st);
-    case 8: return launch_decode<D, 8>(a, st);
-    default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: Hq/Hkv=%d not in {1,2,4,8}", G);
+    default: return launch_decode<D, 8>(a, st);
   }
 }
 
@@ -754,7 +767,8 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
                     hipStream_t st, const PrepArgs* prep = nullptr, const PageArgs* pages = nullptr,
                     const WinArgs* win = nullptr) {
   AILA_REQUIRE(q && k_cache && v_cache && out, "gqa_decode: null pointer");
-  AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hkv <= 65535 && Hq % Hkv == 0,
+  AILA_REQUIRE(B > 0 && B <= 65535 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 &&
+                   static_cast<long>(Hkv) * ((Hq / Hkv + decode_tile(Hq / Hkv) - 1) / decode_tile(Hq / Hkv)) <= 65535,
                "gqa_decode: bad heads/batch (B=%d Hq=%d Hkv=%d)", B, Hq, Hkv);
   AILA_REQUIRE(cached_len >= 0 && cached_len <= max_seq,
                "gqa_decode: cached_len=%d outside [0, max_seq=%d]", cached_len, max_seq);
@@ -764,6 +778,8 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
   a.vc = static_cast<const bf16*>(v_cache);
   a.out = static_cast<bf16*>(out);
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.max_seq = max_seq; a.L = cached_len;
+  a.group = Hq / Hkv;
+  a.chunks = (a.group + decode_tile(a.group) - 1) / decode_tile(a.group);
   a.seq_lens = seq_lens; a.len_bias = len_bias;
   a.k_new = static_cast<const bf16*>(k_new);
   a.v_new = static_cast<const bf16*>(v_new);
@@ -799,7 +815,7 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
     // (one 16-row chunk per wave). Short contexts get one chunk per wave:
     // config 1 (512 rows, 8 KV heads) takes 6.4 us in 8 splits of 64 rows
     // against 7.1 us in 4 of 128.
-    const int groups = B * Hkv;
+    const int groups = B * Hkv * a.chunks;   // workgroups per split
     const int resident = resident_for(D, Hq / Hkv);
     int want = (resident + groups - 1) / groups;
     want = std::max(1, std::min(want, a.nsplit_max));
@@ -812,9 +828,9 @@ int gqa_decode_impl(const void* q, const void* k_cache, const void* v_cache, voi
     a.nsplit = 1;
   }
   switch (D) {
-    case 64: return dispatch_g<64>(Hq / Hkv, a, st);
-    case 128: return dispatch_g<128>(Hq / Hkv, a, st);
-    case 256: return dispatch_g<256>(Hq / Hkv, a, st);
+    case 64: return dispatch_g<64>(a, st);
+    case 128: return dispatch_g<128>(a, st);
+    case 256: return dispatch_g<256>(a, st);
     default: return set_error(AILA_HIP_EUNSUPPORTED, "gqa_decode: D=%d not in {64,128,256}", D);
   }
 }

@@ -93,7 +93,10 @@ size_t aila_hip_gqa_decode_workspace_size(int B, int Hq, int D);
  *               NULL for the single-pass variant (one workgroup per head
  *               group, no split; slower for long contexts).
  * Head h reads KV head h / (Hq / Hkv). Softmax scale 1/sqrt(D).
- * Supported: D in {64, 128, 256}, Hq/Hkv in {1, 2, 4, 8}.
+ * Supported: D in {64, 128, 256}, any integer Hq/Hkv (ratios 1, 2, 4 and 8
+ * map onto the kernel's query-head tile exactly; others run on the next
+ * larger tile, and ratios above 8 on ceil(ratio / 8) workgroups per KV
+ * head, each streaming that head's K/V).
  * Bandwidth note: a head stride max_seq*D*2 that is a multiple of 256 KiB
  * (e.g. max_seq a multiple of 512 rows at D = 256) streams at full rate;
  * an odd row count measured ~7% slower on MI355X. */

@@ -103,10 +103,10 @@ def test_decode_128k_context_device_length():
 def test_decode_rejects_bad_shapes():
     import torch
     import aila_amd
-    q = torch.zeros((1, 12, 128), dtype=torch.bfloat16, device="cuda")
+    q = torch.zeros((1, 10, 128), dtype=torch.bfloat16, device="cuda")
     kc = torch.zeros((1, 4, 64, 128), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(aila_amd.AilaHipError):
-        aila_amd.gqa_decode(q, kc, kc, 10)          # G = 3 unsupported
+        aila_amd.gqa_decode(q, kc, kc, 10)          # 10 query heads over 4 KV heads
     q = torch.zeros((1, 8, 96), dtype=torch.bfloat16, device="cuda")
     kc = torch.zeros((1, 4, 64, 96), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(aila_amd.AilaHipError):

@@ -47,7 +47,7 @@ def _decode_cases():
     cases = []
     for i in range(16):
         D = int(rng.choice([64, 128, 256]))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 8, 12]))
         Hkv = int(rng.choice([1, 2, 4]))
         B = int(rng.integers(1, 6))
         bound = int(rng.integers(64, 3000))
@@ -88,7 +88,7 @@ def _prefill_cases():
     cases = []
     for i in range(16):
         D = int(rng.choice([64, 128, 256]))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 8, 12]))
         Hkv = int(rng.choice([1, 2]))
         S = int(rng.integers(1, 300))
         start = int(rng.integers(0, 2500))
@@ -125,7 +125,7 @@ def _prefill_uncached_cases():
     cases = []
     for i in range(12):
         D = int(rng.choice([64, 128, 256]))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 8, 12]))
         Hkv = int(rng.choice([1, 2]))
         S = int(rng.integers(1, 700))
         cache_pos = int(rng.integers(0, 50))
@@ -249,7 +249,7 @@ def _paged_cases():
     for i in range(12):
         page = int(rng.choice([16, 32, 48, 64, 128, 256]))
         D = int(rng.choice([64, 128, 256]))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 8, 12]))
         B = int(rng.integers(1, 5))
         max_pages = int(rng.integers(2, 12))
         lens = [int(x) for x in rng.integers(1, page * max_pages + 1, size=B)]
@@ -304,7 +304,7 @@ def _fused_prep_cases():
     cases = []
     for i in range(10):
         D = int(rng.choice([64, 128, 256]))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 8, 12]))
         Hkv = int(rng.choice([1, 2, 4]))
         B = int(rng.integers(1, 5))
         rot = int(rng.choice([32, 64, D]))
@@ -422,7 +422,7 @@ def _append_cases():
     cases = []
     for i in range(10):
         D = int(rng.choice([64, 128, 256]))
-        G = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 8, 12]))
         Hkv = int(rng.choice([1, 2, 4]))
         B = int(rng.integers(1, 6))
         max_seq = int(rng.integers(32, 3000))
