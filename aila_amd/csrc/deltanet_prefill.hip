@@ -74,30 +74,46 @@ __device__ __forceinline__ bf16x8_t cat8x2(const u32x2& a, const u32x2& b) {
 __device__ __forceinline__ int swz_rows(int r) { return r & 15; }
 __device__ __forceinline__ int swz_tr(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-// Workspace record of one (sequence, value head, chunk). Every scan operand
-// is stored in register order - [tile][k-step][lane][16 bytes] - so that one
-// wave load is one contiguous KiB (a 16-row gather would cost the memory
-// pipe 16 cache lines per instruction).
-//   W  [4 token tiles][4 k-steps][64][8 bf16]    W[16w+l%16][32ks + slots of l/16]
-//   Kt [8 key tiles][2 token k-steps][64][8 bf16] K[32s2 + slots of l/16][16dt+l%16]
-//   P  [4 token tiles][2 k-steps][64][8 bf16]    P[16w+l%16][32s2 + slots of l/16]
-//   Q  [4 token tiles][4 k-steps][64][8 bf16]    Q[16w+l%16][32ks + slots of l/16]
-//   U  [DV/16 slabs][4 token tiles][64][4 f32]   C layout of U
+// Workspace records of one chunk. Every scan operand is stored in register
+// order - [tile][k-step][lane][16 bytes] - so that one wave load is one
+// contiguous KiB (a 16-row gather would cost the memory pipe 16 cache lines
+// per instruction). The parts that depend on the value head (its gates)
+// are kept per (sequence, value head, chunk):
 //   F  fq[C], fk[C], gamma (f32)
+//   W  [4 token tiles][4 k-steps][64][8 bf16]    W[16w+l%16][32ks + slots of l/16]
 //   WLo  the bf16 residual W - bf16(W), laid out as W
+//   P  [4 token tiles][2 k-steps][64][8 bf16]    P[16w+l%16][32s2 + slots of l/16]
+//   U  [DV/16 slabs][4 token tiles][64][4 f32]   C layout of U
+// and the parts that are copies of the key head's inputs once per
+// (sequence, key head, chunk), written by the key head's first value head
+// and read by all of them:
+//   Kt [8 key tiles][2 token k-steps][64][8 bf16] K[32s2 + slots of l/16][16dt+l%16]
+//   Q  [4 token tiles][4 k-steps][64][8 bf16]    Q[16w+l%16][32ks + slots of l/16]
 //   KtLo (split inputs only) the bf16 residual K - bf16(K), laid out as Kt
-template <int DK, int DV, bool kLo = false>
+// The key-head records follow all value-head records; the workspace sizes
+// them for Hv key heads (Hk <= Hv), so its size does not depend on Hk.
+template <int DK, int DV>
 struct ChunkRec {
   static constexpr size_t kF = 0;
   static constexpr size_t kW = 1024;
   static constexpr size_t kWLo = kW + size_t(kC) * DK * 2;
-  static constexpr size_t kKt = kWLo + size_t(kC) * DK * 2;
-  static constexpr size_t kP = kKt + size_t(DK) * kC * 2;
-  static constexpr size_t kQ = kP + size_t(kC) * kC * 2;
-  static constexpr size_t kU = kQ + size_t(kC) * DK * 2;
-  static constexpr size_t kKtLo = kU + size_t(kC) * DV * 4;
+  static constexpr size_t kP = kWLo + size_t(kC) * DK * 2;
+  static constexpr size_t kU = kP + size_t(kC) * kC * 2;
+  static constexpr size_t kBytes = (kU + size_t(kC) * DV * 4 + 255) / 256 * 256;
+};
+template <int DK, bool kLo = false>
+struct KeyRec {
+  static constexpr size_t kKt = 0;
+  static constexpr size_t kQ = kKt + size_t(DK) * kC * 2;
+  static constexpr size_t kKtLo = kQ + size_t(kC) * DK * 2;
   static constexpr size_t kBytes = (kKtLo + (kLo ? size_t(DK) * kC * 2 : 0) + 255) / 256 * 256;
 };
+// Key-head record (b, hk, c) of a workspace laid out for B, Hv, nch.
+template <int DK, int DV, bool kLo>
+__host__ __device__ __forceinline__ size_t key_rec_offset(int b, int hk, int c, int B, int Hk, int Hv, int nch) {
+  return static_cast<size_t>(B) * Hv * nch * ChunkRec<DK, DV>::kBytes +
+         ((static_cast<size_t>(b) * Hk + hk) * nch + c) * KeyRec<DK, kLo>::kBytes;
+}
 
 // ---------------------------------------------------------------------------
 // kLo: the inputs are fp32 values carried as bf16 hi planes (q, k, v) plus
@@ -117,7 +133,8 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     const bf16* __restrict__ a, const bf16* __restrict__ bg, int ab_stride, const bf16* __restrict__ dt_bias,
     const float* __restrict__ A_log, unsigned char* __restrict__ ws, int T, int Hk, int Hv,
     float eps) {
-  using R = ChunkRec<DK, DV, kLo>;
+  using R = ChunkRec<DK, DV>;
+  using RK = KeyRec<DK, kLo>;
   static_assert(DK == 128 && DV == 128, "tiles of 64 rows x 256 bytes");
   constexpr int RB = DK * 2;       // bytes per K/Q/V row
   constexpr int NC = DK / 8;       // 16-byte chunks per row
@@ -142,6 +159,9 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m16 = lane & 15, g4 = lane >> 4;
   unsigned char* rec = ws + ((static_cast<size_t>(b) * Hv + hv) * nch + c) * R::kBytes;
+  // the key head's first value head writes the key-head record
+  const bool key_writer = hv % (Hv / Hk) == 0;
+  unsigned char* krec = ws + key_rec_offset<DK, DV, kLo>(b, hk, c, static_cast<int>(gridDim.z), Hk, Hv, nch);
 
   // ---- 1. K, Q, V tiles (rows past T are zero) ---------------------------------
   // Split inputs (the layer): thread (cc, r0) forms 16-byte chunk cc of rows
@@ -344,8 +364,8 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
   __syncthreads();
 
   // ---- 2b. Q in register order for the scan (before its tile becomes A) ------
-  {
-    u32x4* Qout = reinterpret_cast<u32x4*>(rec + R::kQ);
+  if (key_writer) {
+    u32x4* Qout = reinterpret_cast<u32x4*>(krec + RK::kQ);
 #pragma unroll
     for (int i = 0; i < kC * DK * 2 / 16 / kThreads; ++i) {
       const int o = i * kThreads + tid;             // [tile][k-step][lane]
@@ -633,8 +653,8 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
     }
   }
   // ---- 6. K^T in slot order over tokens, straight from transposing reads --------
-  {
-    bf16* Ktout = reinterpret_cast<bf16*>(rec + R::kKt);
+  if (key_writer) {
+    bf16* Ktout = reinterpret_cast<bf16*>(krec + RK::kKt);
     // 2 token k-steps x DK/16 key tiles = 16 jobs, 4 per wave
 #pragma unroll
     for (int i = 0; i < 2 * (DK / 16) / 4; ++i) {
@@ -645,7 +665,7 @@ __global__ __launch_bounds__(kThreads, 2) void deltanet_chunk_prep_kernel(
       if constexpr (kLo) {
         const bf16x8_t ol = b_operand(sVW, false, ks, dt);
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4, ol),
-                                    reinterpret_cast<u32x4*>(rec + R::kKtLo + ((dt * 2 + ks) * 64 + lane) * 16));
+                                    reinterpret_cast<u32x4*>(krec + RK::kKtLo + ((dt * 2 + ks) * 64 + lane) * 16));
       }
     }
   }
@@ -688,12 +708,15 @@ template <int DK, int DV, bool kLo>
 __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     const bf16* __restrict__ q, const unsigned char* __restrict__ ws, float* __restrict__ state,
     bf16* __restrict__ out, int T, int Hk, int Hv, float scale) {
-  using R = ChunkRec<DK, DV, kLo>;
+  using R = ChunkRec<DK, DV>;
+  using RK = KeyRec<DK, kLo>;
   static_assert(DK == 4 * 32, "the four state waves own 32 key rows each");
   // XCD-aware placement: workgroups are dispatched round-robin over the 8
   // XCDs, so linear id i runs on XCD i % 8. All DV/16 slabs of one head are
   // put on the same XCD, where they share the head's chunk records in L2
-  // (otherwise every XCD fetches them from HBM).
+  // (otherwise every XCD fetches them from HBM), and each XCD takes a
+  // contiguous range of heads, so that the value heads of a key head also
+  // share its key-head records there.
   constexpr int kSlabs = DV / 16;
   const int nhead = static_cast<int>(gridDim.y * gridDim.z);
   const int lin = blockIdx.x + kSlabs * (blockIdx.y + static_cast<int>(gridDim.y) * blockIdx.z);
@@ -701,7 +724,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
   if (kSlabs == kNumXcd && nhead % kNumXcd == 0) {
     const int xcd = lin % kNumXcd, i = lin / kNumXcd;
     slab = i % kSlabs;
-    headlin = xcd + kNumXcd * (i / kSlabs);
+    headlin = xcd * (nhead / kNumXcd) + i / kSlabs;
   }
   const int hv = headlin % Hv, b = headlin / Hv;
   const int nch = (T + kC - 1) / kC;
@@ -719,6 +742,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
 
   const unsigned char* recs = ws + (static_cast<size_t>(b) * Hv + hv) * nch * R::kBytes;
   auto rec_of = [&](int c) __attribute__((always_inline)) { return recs + static_cast<size_t>(c) * R::kBytes; };
+  const unsigned char* krecs =
+      ws + key_rec_offset<DK, DV, kLo>(b, hv / (Hv / Hk), 0, static_cast<int>(gridDim.z), Hk, Hv, nch);
+  auto krec_of = [&](int c) __attribute__((always_inline)) { return krecs + static_cast<size_t>(c) * RK::kBytes; };
 
   if (wave < 4) {
     // ------------------------------------------------------------ state waves
@@ -735,7 +761,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
         o.wl[part] = reinterpret_cast<const u32x4*>(rec + R::kWLo)[(w4 * 4 + part) * 64 + lane];
       } else if (part < 6) {
         const int tt = part - 4;
-        const u32x4* Kt = reinterpret_cast<const u32x4*>(rec + R::kKt) + lane;
+        const u32x4* Kt = reinterpret_cast<const u32x4*>(krec_of(c) + RK::kKt) + lane;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) o.kt[tt][s2] = Kt[((w4 * 2 + tt) * 2 + s2) * 64];
       } else if (part == 6) {
@@ -774,7 +800,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
       // chunk ahead of its use) instead of in the rotating sets
       u32x4 ktl[2][2];
       if constexpr (kLo) {
-        const u32x4* Ktl = reinterpret_cast<const u32x4*>(rec_of(min(cc, nch - 1)) + R::kKtLo) + lane;
+        const u32x4* Ktl = reinterpret_cast<const u32x4*>(krec_of(min(cc, nch - 1)) + RK::kKtLo) + lane;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -875,7 +901,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deltanet_chunk_scan_kernel(
     auto load = [&](int c, OutOps& o, int part) __attribute__((always_inline)) {
       const unsigned char* rec = rec_of(c);
       if (part < 4) {
-        o.q[part] = reinterpret_cast<const u32x4*>(rec + R::kQ)[(w4 * 4 + part) * 64 + lane];
+        o.q[part] = reinterpret_cast<const u32x4*>(krec_of(c) + RK::kQ)[(w4 * 4 + part) * 64 + lane];
       } else {
         const u32x4* P = reinterpret_cast<const u32x4*>(rec + R::kP) + w4 * 2 * 64 + lane;
         o.p[0] = P[0];
@@ -947,7 +973,8 @@ namespace aila {
 // entry point (bf16 inputs) and the full layer (split fp32 inputs).
 size_t deltanet_chunk_records_bytes(int B, int T, int Hv, bool split) {
   const size_t nch = (static_cast<size_t>(T) + kC - 1) / kC;
-  return static_cast<size_t>(B) * Hv * nch * (split ? ChunkRec<128, 128, true>::kBytes : ChunkRec<128, 128, false>::kBytes);
+  return static_cast<size_t>(B) * Hv * nch *
+         (ChunkRec<128, 128>::kBytes + (split ? KeyRec<128, true>::kBytes : KeyRec<128, false>::kBytes));
 }
 
 // conv == nullptr: q, k, v planes (bf16 inputs). Otherwise the layer: q, k,
