@@ -387,7 +387,8 @@ int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,
 
 /* Workspace bytes for aila_hip_deltanet_prefill (per-chunk W and its
  * residual, U, P, Q, K^T and decay factors, in the scan's operand order;
- * 105 KiB per (sequence, value head, 64-token chunk)). 0 for the shapes that
+ * 105 KiB per (sequence, value head, 64-token chunk), of which the key
+ * head's K^T and Q parts are used once per key head). 0 for the shapes that
  * run the general-shape kernel. */
 size_t aila_hip_deltanet_prefill_workspace_size(int B, int T, int Hv, int dk,
                                                 int dv);
