@@ -74,7 +74,7 @@ def test_decode_shapes(D, G):
     _decode_case(1000 + D + G, 2, Hkv * G, Hkv, D, 1100, 1037, split=True)
 
 
-@pytest.mark.parametrize("L", [1, 15, 16, 17, 127, 128, 129, 4095])
+@pytest.mark.parametrize("L", [1, 15, 16, 17, 127, 128, 129, 4095, 4096, 6001, 8192])
 def test_decode_lengths(L):
     _decode_case(2000 + L, 1, 16, 4, 256, L + 33, L, split=True)
 
