@@ -7,13 +7,13 @@
 // state column slab lives in VGPRs between the two reductions.
 //
 // Work decomposition: one 256-thread workgroup per (value head, sequence,
-// slab of 4*CQ columns of dv), CQ = 32 or 16. Thread t owns columns
+// slab of 4*CQ columns of dv), CQ = 32, 16 or 8. Thread t owns columns
 // 4*(t%CQ)..+3 of the slab and rows (t/CQ)*RPT..+RPT-1 of dk (RPT = dk /
 // (256/CQ)). Loads are float4 along dv, so a wave reads 512- or 256-byte row
 // segments per instruction. The column sums u = S^T k and o = S^T q are
 // reduced over the row groups of a wave with lane swaps and over the 4
-// waves through LDS. The narrower slab (CQ = 16) doubles the workgroups for
-// small batches, where one workgroup per CU leaves the state load latency
+// waves through LDS. The narrower slabs (CQ = 16, 8) multiply the workgroups
+// for small batches, where one workgroup per CU leaves the state load latency
 // exposed (Hv = 32, dk = dv = 128, B = 8: 7.14 -> 6.70 us).
 // State loads and stores are nontemporal: each step touches the state once
 // and the next touch of the same state comes after every other layer's
@@ -212,8 +212,12 @@ extern "C" int aila_hip_deltanet_decode(const void* q, const void* k,
   const bf16* bp = static_cast<const bf16*>(b);
   const bf16* dtp = static_cast<const bf16*>(dt_bias);
   bf16* op = static_cast<bf16*>(out);
-  // 128-column slabs unless that leaves fewer than two workgroups per CU.
-  const bool narrow = static_cast<long>(B) * Hv * ((dv + 127) / 128) < 512;
+  // 128-column slabs unless that leaves fewer than two workgroups per CU;
+  // 32-column slabs when even 64-column ones leave CUs idle (batch 1-4 of
+  // 32 value heads: B=1 4.1 -> 3.9 us, B=2 4.3 -> 4.15 us).
+  const long heads = static_cast<long>(B) * Hv * ((dv + 127) / 128);
+  const bool narrow = heads < 512;
+  const bool narrower = heads <= 128;
   auto launch = [&](auto dk_tag, auto cq_tag) {
     constexpr int DK = decltype(dk_tag)::value, CQ = decltype(cq_tag)::value;
     const dim3 grid(Hv, B, (dv + CQ * 4 - 1) / (CQ * 4));
@@ -221,7 +225,8 @@ extern "C" int aila_hip_deltanet_decode(const void* q, const void* k,
                        A_log, state, op, Hk, Hv, dv, eps, scale);
   };
   auto with_cq = [&](auto dk_tag) {
-    if (narrow) launch(dk_tag, std::integral_constant<int, 16>{});
+    if (narrower) launch(dk_tag, std::integral_constant<int, 8>{});
+    else if (narrow) launch(dk_tag, std::integral_constant<int, 16>{});
     else launch(dk_tag, std::integral_constant<int, 32>{});
   };
   switch (dk) {
