@@ -417,7 +417,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
 
   // ---- fused copy_to_cache: this pair's own K/V rows, shared by the G query
   //      heads of the KV group (head h copies every G-th row from h % G).
-  auto copy_rows_to_cache = [&]() __attribute__((always_inline)) {
+  auto copy_rows_to_cache = [&](int tid0, int nthr) __attribute__((always_inline)) {
     if (k_cache != nullptr) {
       const int gi = h % G;
 #pragma unroll 1
@@ -426,7 +426,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
         if (pass == 1 && ql == qh) break;
         const int r0 = qb * C::BM, r1 = min(r0 + C::BM, S);
         const int nrow = (r1 - r0 - gi + G - 1) / G;   // rows r0 + gi, r0 + gi + G, ...
-        for (int p = threadIdx.x; p < nrow * C::NC; p += 2 * kThreads) {
+        for (int p = tid0; p < nrow * C::NC; p += nthr) {
           const int row = r0 + gi + (p / C::NC) * G, c = p % C::NC;
           const size_t src = static_cast<size_t>(row) * kv_row_stride + c * 8;
           const size_t dst = (static_cast<size_t>(kvh) * max_seq + cache_pos + row) * D + c * 8;
@@ -490,7 +490,13 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
     step(j, sK0[grp], sV1[grp]);
     if (j + 1 <= nsteps) step(j + 1, sK1[grp], sV0[grp]);
   }
-  if (grp == 0) phase_barrier();
+  // Group A copies the pair's K/V rows to the cache while group B runs its
+  // last matrix phase (config 2: 43.7 -> 43.3 us against all 512 threads
+  // copying after the merge).
+  if (grp == 0) {
+    copy_rows_to_cache(t, kThreads);
+    phase_barrier();
+  }
 
   // ---- finish: light block of A, heavy block (merged when split) -------------
   __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
@@ -549,7 +555,6 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   } else if (b_has_heavy && grp == 1) {
     store_segment();
   }
-  copy_rows_to_cache();
 }
 
 // Key-split merge: out row = sum_z 2^(m_z - M) acc_z / sum_z 2^(m_z - M) l_z
