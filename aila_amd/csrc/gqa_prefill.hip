@@ -691,16 +691,36 @@ size_t key_split_bytes(int nz, int S, int Hq, int D) {
   return static_cast<size_t>(nz) * Hq * S * (D + 4) * sizeof(float);
 }
 
+// Short sequences and few heads leave most CUs idle with 32 query rows per
+// wave (one workgroup per balanced pair of 128-row blocks and head). When
+// 16 rows per wave (64-row blocks, twice the workgroups, twice the LDS
+// operand bytes per MFMA) still fits one round of the device, it is faster
+// (Hq=32, Hkv=8, D=128: S=512 20.4 -> 13.5 us, S=1024 28.5 -> 20.8;
+// Hq=8, Hkv=2, S=4096 65.4 -> 47.5); two rounds are slower (S=1280: 32.0
+// against 40.2), so larger grids keep 32 rows per wave.
+template <int D>
+bool short_prefill(int S, int Hq, int nz) {
+  if (nz > 1) return false;
+  const long npair16 = ((S + 63) / 64 + 1) / 2;
+  return npair16 * Hq <= prefill_resident<D>();
+}
+
 int dispatch_prefill(int D, const bf16* q, const bf16* k, const bf16* v, int kv_row_stride,
                      long kv_head_stride, bf16* out, int S, int start_pos, int Hq, int Hkv,
                      bf16* k_cache, bf16* v_cache, int cache_pos, int max_seq, hipStream_t st,
                      int nz = 1, float* part = nullptr) {
   switch (D) {
     case 64:
+      if (short_prefill<64>(S, Hq, nz))
+        return launch_prefill<64, 16, 64>(q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache,
+                                          v_cache, cache_pos, max_seq, nz, part, st);
       return launch_prefill<64, PrefillShape<64>::RPW, PrefillShape<64>::BN>(
           q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache, v_cache, cache_pos, max_seq,
           nz, part, st);
     case 128:
+      if (short_prefill<128>(S, Hq, nz))
+        return launch_prefill<128, 16, 64>(q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache,
+                                           v_cache, cache_pos, max_seq, nz, part, st);
       return launch_prefill<128, PrefillShape<128>::RPW, PrefillShape<128>::BN>(
           q, k, v, kv_row_stride, kv_head_stride, out, S, start_pos, Hq, Hkv, k_cache, v_cache, cache_pos, max_seq,
           nz, part, st);
