@@ -697,12 +697,17 @@ size_t key_split_bytes(int nz, int S, int Hq, int D) {
 // operand bytes per MFMA) still fits one round of the device, it is faster
 // (Hq=32, Hkv=8, D=128: S=512 20.4 -> 13.5 us, S=1024 28.5 -> 20.8;
 // Hq=8, Hkv=2, S=4096 65.4 -> 47.5); two rounds are slower (S=1280: 32.0
-// against 40.2), so larger grids keep 32 rows per wave.
+// against 40.2), so larger grids keep 32 rows per wave. So does a
+// sequence that gets no more workgroups from it (S = 65..128: one pair
+// either way, and over a 4096-row cached prefix 81 against 64 us), unless
+// the 128-row block would be half padding (S <= 64: 61 -> 43 us over the
+// same prefix).
 template <int D>
 bool short_prefill(int S, int Hq, int nz) {
   if (nz > 1) return false;
   const long npair16 = ((S + 63) / 64 + 1) / 2;
-  return npair16 * Hq <= prefill_resident<D>();
+  const long npair32 = ((S + 127) / 128 + 1) / 2;
+  return (npair16 > npair32 || S <= 64) && npair16 * Hq <= prefill_resident<D>();
 }
 
 int dispatch_prefill(int D, const bf16* q, const bf16* k, const bf16* v, int kv_row_stride,
