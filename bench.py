@@ -1029,6 +1029,74 @@ def sub_decode_cfg1(torch, aila_amd, per_graph=32, reps=20):
             "GBps": round(byts / us / 1e3, 1)}
 
 
+def sub_single_sequence(torch, aila_amd, per_graph=8, reps=20):
+    """The reference engine runs one sequence at a time: the path's kernels
+    at batch 1 and for short prompts (the Qwen3.5-4B and Qwen3-4B shapes),
+    each timed by HIP-graph replay. Not a config of the benchmark; reported
+    beside it."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 6)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(per_graph):
+                fn()
+        gr.replay()
+        return round(time_graph(torch, gr, reps) * 1e3 / per_graph, 2)
+
+    res = {"note": "batch 1 and short prompts (the reference's single-sequence use); us per call, graph replay"}
+    for L in (8192, 32768):   # Qwen3.5 full-attention layer decode
+        Hq, Hkv, D = GQA_HQ, GQA_HKV, GQA_D
+        q = torch.randn((1, Hq, D), generator=g, **bf)
+        kc = torch.randn((1, Hkv, L, D), generator=g, **bf)
+        vc = torch.randn_like(kc)
+        ws = torch.empty(aila_amd.gqa_decode_workspace_size(1, Hq, D), dtype=torch.uint8, device="cuda")
+        out = torch.empty_like(q)
+        us = timed(lambda: aila_amd.gqa_decode(q, kc, vc, L, out=out, workspace=ws))
+        res[f"gqa_decode_B1_L{L}_16q4kv_D256"] = {"us": us, "GBps": round(gqa_bytes(1, Hq, Hkv, D, L) / us / 1e3, 1)}
+        del kc, vc
+    for S, Hq, Hkv, D in ((512, 32, 8, 128), (512, GQA_HQ, GQA_HKV, GQA_D)):   # prompt prefill
+        qq = torch.randn((S, Hq * D), generator=g, **bf)
+        kk = torch.randn((S, Hkv * D), generator=g, **bf)
+        vv = torch.randn((S, Hkv * D), generator=g, **bf)
+        o = torch.empty_like(qq)
+        us = timed(lambda: aila_amd.gqa_prefill(qq, kk, vv, Hq, Hkv, out=o))
+        res[f"gqa_prefill_S{S}_{Hq}q{Hkv}kv_D{D}"] = {"us": us,
+                                                       "tflops": round(4 * D * Hq * S * (S + 1) / 2 / us / 1e6, 1)}
+    Hk, Hv, d = DN_HK, DN_HV, DN_D
+    st = torch.empty((1, Hv, d, d), dtype=torch.float32, device="cuda").normal_(0, 0.02, generator=g)
+    q = torch.randn((1, Hk, d), generator=g, **bf)
+    k = torch.randn((1, Hk, d), generator=g, **bf)
+    v = torch.randn((1, Hv, d), generator=g, **bf)
+    a = torch.randn((1, Hv), generator=g, **bf)
+    b = torch.randn((1, Hv), generator=g, **bf)
+    o = torch.empty((1, Hv, d), **bf)
+    res["deltanet_decode_B1"] = {"us": timed(lambda: aila_amd.deltanet_decode(q, k, v, a, b, st, out=o))}
+    ch = 2 * Hk * d + Hv * d
+    cs = torch.empty((1, 3, ch), dtype=torch.float32, device="cuda").normal_(generator=g)
+    w = torch.randn((ch, 4), generator=g, **bf)
+    nw = torch.ones(d, dtype=torch.float32, device="cuda")
+    arr = torch.zeros((Hk,), dtype=torch.int32, device="cuda")
+    heads = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    x = dict(qkv=torch.randn((1, ch), generator=g, **bf), z=torch.randn((1, Hv * d), generator=g, **bf))
+    lo = torch.empty((1, Hv * d), **bf)
+    res["deltanet_layer_decode_B1"] = {"us": timed(lambda: aila_amd.deltanet_layer_decode(
+        x["qkv"], x["z"], a, b, w, cs, 0, nw, st, Hk, out=lo, conv_heads=heads, arrivals=arr))}
+    T = 512
+    fused = torch.randn((1, T, ch + Hv * d + 2 * Hv), generator=g, **bf)
+    lws = torch.empty(aila_amd.deltanet_layer_prefill_workspace_size(1, T, Hk, Hv), dtype=torch.uint8, device="cuda")
+    lout = torch.empty((1, T, Hv * d), **bf)
+    zc, ac = ch + Hv * d, ch + Hv * d + Hv
+    res[f"deltanet_layer_prefill_T{T}"] = {"us": timed(lambda: aila_amd.deltanet_layer_prefill(
+        fused[:, :, :ch], fused[:, :, ch:zc], fused[:, :, zc:ac], fused[:, :, ac:], w, cs, 0, nw, st, Hk, out=lout,
+        workspace=lws))}
+    return res
+
+
 # ------------------------------------------------------------ CPU baseline --
 def cpu_baseline(min_seconds=10.0):
     """The scalar oracle (fast-math build, OpenMP over heads) on the host
@@ -1160,7 +1228,7 @@ def main():
     ap.add_argument("--profile-kernel", nargs="?", const="gqa_decode", default=None,
                     choices=["gqa_decode", "gqa_prefill", "deltanet_decode", "deltanet_prefill", "paged_decode",
                              "deltanet_layer_decode", "deltanet_layer_prefill", "decode_prep", "fused_prep_decode",
-                             "stack", "stack_full", "prefill_cached"],
+                             "stack", "stack_full", "prefill_cached", "single_sequence"],
                     help="only run one kernel 20 times (default: the dominant config-5 GQA decode "
                          "layer, plus a 1 GiB device copy for counter calibration), for rocprofv3")
     ap.add_argument("--write-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -1189,6 +1257,7 @@ def main():
          "paged_decode": lambda t, a: sub_paged_decode(t, a),
          "fused_prep_decode": lambda t, a: sub_fused_prep_decode(t, a),
          "prefill_cached": lambda t, a: sub_prefill_cached(t, a),
+         "single_sequence": lambda t, a: sub_single_sequence(t, a),
          "stack": lambda t, a: {k: v for k, v in bench_config5(t, a, 32, 4).items() if k != "W"},
          "stack_full": lambda t, a: bench_config5_full_layers(t, a, build_config5(t, a, 32, 4), 32, 4),
          }[args.profile_kernel](torch, aila_amd)
@@ -1230,6 +1299,8 @@ def main():
         log(f"[bench] decode prep {sub['decode_prep']}")
         sub["fused_prep_decode"] = sub_fused_prep_decode(torch, aila_amd)
         log(f"[bench] fused prep+decode {sub['fused_prep_decode']}")
+        sub["single_sequence"] = sub_single_sequence(torch, aila_amd)
+        log(f"[bench] single sequence {sub['single_sequence']}")
         log(f"[bench] decode cfg1 {sub['gqa_decode_cfg1']}")
     cpu = None
     if not args.no_cpu:
