@@ -12,7 +12,8 @@ Attention outputs within max relative error 1e-2, DeltaNet states within
 1e-3; cache rows and pool pages past the attended range hold NaN.
 
 AILA_SWEEP_SEED=n draws another set of cases (default 0: the set the suite
-runs by default)."""
+runs by default); a range "a-b" or a list "a,b,c" runs the sets of several
+seeds in one process."""
 import os
 
 import numpy as np
@@ -23,7 +24,25 @@ from aila_amd import datagen as dg
 
 pytestmark = pytest.mark.gpu
 ATTN_TOL = 1e-2
-SWEEP_SEED = int(os.environ.get("AILA_SWEEP_SEED", "0"))
+
+
+def _parse_seeds(text):
+    seeds = []
+    for part in text.split(","):
+        part = part.strip()
+        if "-" in part:
+            lo, hi = (int(x) for x in part.split("-", 1))
+            seeds.extend(range(lo, hi + 1))
+        elif part:
+            seeds.append(int(part))
+    return seeds or [0]
+
+
+SWEEP_SEEDS = _parse_seeds(os.environ.get("AILA_SWEEP_SEED", "0"))
+
+
+def _all(gen):
+    return [case for seed in SWEEP_SEEDS for case in gen(seed)]
 
 
 def _t(x):
@@ -42,8 +61,8 @@ def _relerr(a, r):
     return float(np.max(np.abs(a - r)) / max(float(np.max(np.abs(r))), 1e-30))
 
 
-def _decode_cases():
-    rng = np.random.default_rng(0x5EE9 + SWEEP_SEED)
+def _decode_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EE9 + sweep_seed)
     cases = []
     for i in range(16):
         D = int(rng.choice([64, 128, 256]))
@@ -57,7 +76,7 @@ def _decode_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,D,G,Hkv,B,bound,lens", _decode_cases())
+@pytest.mark.parametrize("i,D,G,Hkv,B,bound,lens", _all(_decode_cases))
 def test_sweep_decode_device_lengths(i, D, G, Hkv, B, bound, lens):
     import torch
     import aila_amd
@@ -83,8 +102,8 @@ def test_sweep_decode_device_lengths(i, D, G, Hkv, B, bound, lens):
         assert _relerr(got[b], want) <= ATTN_TOL, (b, L)
 
 
-def _prefill_cases():
-    rng = np.random.default_rng(0x5EEA + SWEEP_SEED)
+def _prefill_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EEA + sweep_seed)
     cases = []
     for i in range(16):
         D = int(rng.choice([64, 128, 256]))
@@ -96,7 +115,7 @@ def _prefill_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,D,G,Hkv,S,start", _prefill_cases())
+@pytest.mark.parametrize("i,D,G,Hkv,S,start", _all(_prefill_cases))
 def test_sweep_prefill_cached(i, D, G, Hkv, S, start):
     import torch
     import aila_amd
@@ -120,8 +139,8 @@ def test_sweep_prefill_cached(i, D, G, Hkv, S, start):
         assert _relerr(got, want) <= ATTN_TOL, ("split" if w is not None and need else "whole")
 
 
-def _prefill_uncached_cases():
-    rng = np.random.default_rng(0x5EEB + SWEEP_SEED)
+def _prefill_uncached_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EEB + sweep_seed)
     cases = []
     for i in range(12):
         D = int(rng.choice([64, 128, 256]))
@@ -133,7 +152,7 @@ def _prefill_uncached_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,D,G,Hkv,S,cache_pos", _prefill_uncached_cases())
+@pytest.mark.parametrize("i,D,G,Hkv,S,cache_pos", _all(_prefill_uncached_cases))
 def test_sweep_prefill_with_cache_write(i, D, G, Hkv, S, cache_pos):
     """Causal prefill (AttentionOps.cpp:649-842) with the fused cache write
     (copy_to_cache, :2513-2532): output within tolerance, cache bit-exact."""
@@ -161,8 +180,8 @@ def test_sweep_prefill_with_cache_write(i, D, G, Hkv, S, cache_pos):
     assert np.array_equal(_np(kc), ck) and np.array_equal(_np(vc), cv)
 
 
-def _deltanet_prefill_cases():
-    rng = np.random.default_rng(0x5EEC + SWEEP_SEED)
+def _deltanet_prefill_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EEC + sweep_seed)
     cases = []
     for i in range(12):
         B = int(rng.integers(1, 4))
@@ -175,7 +194,7 @@ def _deltanet_prefill_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,B,T,Hk,Hv,gates,s0", _deltanet_prefill_cases())
+@pytest.mark.parametrize("i,B,T,Hk,Hv,gates,s0", _all(_deltanet_prefill_cases))
 def test_sweep_deltanet_prefill(i, B, T, Hk, Hv, gates, s0):
     """Chunked prefill against the sequential recurrence
     (Qwen35HybridTextBackend.cpp:1729-1780): outputs 1e-2, state 1e-3."""
@@ -204,8 +223,8 @@ def test_sweep_deltanet_prefill(i, B, T, Hk, Hv, gates, s0):
     assert _relerr(got_S, want_S) <= 1e-3
 
 
-def _deltanet_decode_cases():
-    rng = np.random.default_rng(0x5EED + SWEEP_SEED)
+def _deltanet_decode_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EED + sweep_seed)
     cases = []
     for i in range(12):
         dk = int(rng.choice([64, 128, 256]))
@@ -217,7 +236,7 @@ def _deltanet_decode_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,B,Hk,Hv,dk,dv", _deltanet_decode_cases())
+@pytest.mark.parametrize("i,B,Hk,Hv,dk,dv", _all(_deltanet_decode_cases))
 def test_sweep_deltanet_decode(i, B, Hk, Hv, dk, dv):
     """Recurrent decode steps (Qwen35HybridTextBackend.cpp:1094-1148) against
     the sequential oracle over 4 steps."""
@@ -243,8 +262,8 @@ def test_sweep_deltanet_decode(i, B, Hk, Hv, dk, dv):
     assert _relerr(got_o, dg.bf16_to_f32(want_ob)) <= ATTN_TOL
 
 
-def _paged_cases():
-    rng = np.random.default_rng(0x5EEE + SWEEP_SEED)
+def _paged_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EEE + sweep_seed)
     cases = []
     for i in range(12):
         page = int(rng.choice([16, 32, 48, 64, 128, 256]))
@@ -257,7 +276,7 @@ def _paged_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,page,D,G,B,max_pages,lens", _paged_cases())
+@pytest.mark.parametrize("i,page,D,G,B,max_pages,lens", _all(_paged_cases))
 def test_sweep_paged_decode(i, page, D, G, B, max_pages, lens):
     """Paged decode equals the contiguous decode of the same rows bit for
     bit and the oracle within tolerance; unowned pool pages hold NaN."""
@@ -299,8 +318,8 @@ def test_sweep_paged_decode(i, page, D, G, B, max_pages, lens):
         assert _relerr(g[b], want) <= ATTN_TOL, (b, L)
 
 
-def _fused_prep_cases():
-    rng = np.random.default_rng(0x5EEF + SWEEP_SEED)
+def _fused_prep_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EEF + sweep_seed)
     cases = []
     for i in range(10):
         D = int(rng.choice([64, 128, 256]))
@@ -316,7 +335,7 @@ def _fused_prep_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,D,G,Hkv,B,rot,packed,split,max_seq,pos", _fused_prep_cases())
+@pytest.mark.parametrize("i,D,G,Hkv,B,rot,packed,split,max_seq,pos", _all(_fused_prep_cases))
 def test_sweep_fused_prepare_append_decode(i, D, G, Hkv, B, rot, packed, split, max_seq, pos):
     """One launch of QK-norm + RoPE + K/V append + decode at device positions
     (decode_prepare_qkv, ElementwiseOps.cpp:105-216, then attention_decode)
@@ -357,8 +376,8 @@ def test_sweep_fused_prepare_append_decode(i, D, G, Hkv, B, rot, packed, split, 
         assert np.array_equal(_np(res[1]), gw)
 
 
-def _layer_cases():
-    rng = np.random.default_rng(0x5EF1 + SWEEP_SEED)
+def _layer_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EF1 + sweep_seed)
     cases = []
     for i in range(8):
         B = int(rng.integers(1, 4))
@@ -372,7 +391,7 @@ def _layer_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,B,Hk,Hv,T,steps,head0,wide", _layer_cases())
+@pytest.mark.parametrize("i,B,Hk,Hv,T,steps,head0,wide", _all(_layer_cases))
 def test_sweep_layer_prefill_then_decode(i, B, Hk, Hv, T, steps, head0, wide):
     """Whole DeltaNet layer (conv ring + SiLU, L2 norms, recurrence, gated
     RMSNorm; Qwen35HybridTextBackend.cpp:1640-1798): a T-token prefill, then
@@ -417,8 +436,8 @@ def test_sweep_layer_prefill_then_decode(i, B, Hk, Hv, T, steps, head0, wide):
         assert not arr.any()
 
 
-def _append_cases():
-    rng = np.random.default_rng(0x5EF2 + SWEEP_SEED)
+def _append_cases(sweep_seed):
+    rng = np.random.default_rng(0x5EF2 + sweep_seed)
     cases = []
     for i in range(10):
         D = int(rng.choice([64, 128, 256]))
@@ -432,7 +451,7 @@ def _append_cases():
     return cases
 
 
-@pytest.mark.parametrize("i,D,G,Hkv,B,max_seq,bound,pos", _append_cases())
+@pytest.mark.parametrize("i,D,G,Hkv,B,max_seq,bound,pos", _all(_append_cases))
 def test_sweep_decode_append_device_positions(i, D, G, Hkv, B, max_seq, bound, pos):
     """Append + split-K decode in one launch at device positions under a host
     bound (ElementwiseOps.cpp:105-216 cache write, then
