@@ -65,6 +65,13 @@ def test_prefill_config4_qwen35():
     _case(0xA11A + 3, 1, 4096, 16, 32, s0_std=0.0)
 
 
+def test_prefill_long_sequence():
+    # 32k tokens (512 chunks) through one head pair: the state is carried
+    # across the whole chain within 1e-3, outputs within 1e-2.
+    print("deltanet prefill T=32768 Hk=1 Hv=2", flush=True)
+    _case(0xA11A + 40, 1, 32768, 1, 2, gates=True)
+
+
 @pytest.mark.parametrize("T", [1, 5, 63, 64, 65, 130, 200])
 def test_prefill_ragged_lengths(T):
     _case(8000 + T, 2, T, 2, 4, gates=True)

@@ -242,3 +242,78 @@ def test_prefill_rejects_bad_args():
     cache = torch.zeros((2, 20, 128), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(aila_amd.AilaHipError):
         aila_amd.gqa_prefill(q, kv, kv, 8, 2, k_cache=cache, v_cache=cache, cache_pos=10)
+
+
+def _sampled_rows(S, extra=()):
+    """Rows at the ends of 64- and 128-row blocks, the first and last rows
+    and a few spread through the prompt."""
+    rows = {0, 1, 63, 64, 127, 128, 129, S // 3, S // 2 + 17, S - 129, S - 128, S - 65, S - 2, S - 1, *extra}
+    return sorted(r for r in rows if 0 <= r < S)
+
+
+def _rows_against_decode(q, kc, vc, got, rows, base, Hq, Hkv, D, max_seq):
+    """Row r of a causal prefill whose first row sits at position `base` is a
+    decode of that query over cache rows [0, base + r] (AttentionOps.cpp:73-166
+    against :649-842 / :2308-2507)."""
+    worst = 0.0
+    for r in rows:
+        qr = q[r].reshape(1, Hq, D)
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(qr, kc[None], vc[None], 1, Hq, Hkv, D, max_seq,
+                                                               base + r + 1))[0].reshape(-1)
+        err = _relerr(got[r], want)
+        assert err <= ATTN_TOL, (r, err)
+        worst = max(worst, err)
+    return worst
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,D", [(16384, 4, 1, 128), (8192, 4, 2, 256), (12000, 2, 1, 64)])
+def test_prefill_long_prompt_rows_match_decode(S, Hq, Hkv, D):
+    """Prompts of 8k-16k tokens (the naive oracle prefill would take minutes
+    at these sizes): sampled rows against the oracle's decode over the same
+    rows, every output finite, and the fused cache write bit-exact."""
+    import torch
+    import aila_amd
+    seed = 7600 + S + D
+    print(f"long prefill S={S} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    q, k, v = qk_prepped(seed, S, Hq, Hkv, D)
+    max_seq = S + 3
+    kc = torch.full((Hkv, max_seq, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    vc = torch.full((Hkv, max_seq, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    out = aila_amd.gqa_prefill(_t(q), _t(k), _t(v), Hq, Hkv, k_cache=kc, v_cache=vc, cache_pos=0)
+    torch.cuda.synchronize()
+    got = dg.bf16_to_f32(_np(out))
+    assert np.isfinite(got).all()
+    ck, cv = _np(kc), _np(vc)
+    seven = dg.f32_to_bf16(np.float32([7.0]))[0]
+    assert np.array_equal(ck[:, :S], k.reshape(S, Hkv, D).transpose(1, 0, 2))
+    assert np.array_equal(cv[:, :S], v.reshape(S, Hkv, D).transpose(1, 0, 2))
+    assert (ck[:, S:] == seven).all() and (cv[:, S:] == seven).all()
+    _rows_against_decode(q, ck, cv, got, _sampled_rows(S), 0, Hq, Hkv, D, max_seq)
+
+
+@pytest.mark.parametrize("S,start,Hq,Hkv,D", [(512, 30000, 16, 4, 256), (300, 60000, 8, 1, 128)])
+def test_prefill_cached_long_prefix_rows_match_decode(S, start, Hq, Hkv, D):
+    """A turn over a 30k-60k-row cached prefix, with the key split (4 and 16
+    runs) and without a workspace: sampled rows against the oracle's decode over
+    the cache rows each row attends, NaN poison past the attended range."""
+    import torch
+    import aila_amd
+    seed = 7700 + S + D
+    max_seq = start + S + 9
+    print(f"cached long prefix S={S} start={start} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    kc = dg.normal_bf16(seed, 1, (Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 2, (Hkv, max_seq, D))
+    kc[:, start + S:] = 0x7FC0
+    vc[:, start + S:] = 0x7FC0
+    q = dg.normal_bf16(seed, 0, (S, Hq * D))
+    need = aila_amd.gqa_prefill_cached_workspace_size(S, start, Hq, Hkv, D)
+    dq, dk, dv = _t(q), _t(kc), _t(vc)
+    rows = _sampled_rows(S)
+    for ws_bytes in (need, 0):
+        ws = None
+        if ws_bytes:
+            ws = torch.full((ws_bytes // 4,), float("nan"), dtype=torch.float32, device="cuda").view(torch.uint8)
+        got = dg.bf16_to_f32(_np(aila_amd.gqa_prefill_cached(dq, dk, dv, start, Hq, workspace=ws)))
+        torch.cuda.synchronize()
+        assert np.isfinite(got).all(), ws_bytes
+        _rows_against_decode(q, kc, vc, got, rows, start, Hq, Hkv, D, max_seq)
