@@ -4,6 +4,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <cmath>
 #include <stdint.h>
 #include <math.h>
 
@@ -248,10 +250,37 @@ __device__ __forceinline__ RowPos rope_row_pos(const RopePos& rp, int b, int row
   return p;
 }
 
-// Inverse frequency of rotary pair j: the caller's table, or
-// theta^(-2j/rot).
-__device__ __forceinline__ float rope_inv_freq(const RopePos& rp, int j, int rot, float theta) {
-  return rp.inv_freq ? rp.inv_freq[j] : 1.0f / powf(theta, (2.0f * j) / static_cast<float>(rot));
+// Inverse rotary frequencies 1 / theta^(2j/rot), j < rot/2, formed on the
+// host with the power correctly rounded to float (double pow, rounded once)
+// and passed by value in the kernel arguments. The device powf is not
+// correctly rounded: a frequency one ulp off turns pair j's angle at
+// position p by p times that ulp (relative output error ~3e-2 at p = 1M),
+// where the reference's formula 1 / pow(theta, 2j/rot) with a correctly
+// rounded pow (ElementwiseOps.cpp:80) gives the float the host computes.
+constexpr int kMaxRopePairs = 128;   // rot <= D <= 256
+struct RopeFreq {
+  float f[kMaxRopePairs];
+};
+
+inline RopeFreq rope_freq_table(float theta, int rot) {
+  thread_local float last_theta = 0.f;
+  thread_local int last_rot = 0;
+  thread_local RopeFreq last{};
+  if (theta != last_theta || rot != last_rot) {
+    for (int j = 0; j < rot / 2 && j < kMaxRopePairs; ++j) {
+      const float x = (2.0f * static_cast<float>(j)) / static_cast<float>(rot);
+      const float p = static_cast<float>(std::pow(static_cast<double>(theta), static_cast<double>(x)));
+      last.f[j] = 1.0f / p;
+    }
+    last_theta = theta;
+    last_rot = rot;
+  }
+  return last;
+}
+
+// Inverse frequency of rotary pair j: the caller's table, or the host's.
+__device__ __forceinline__ float rope_inv_freq(const RopePos& rp, const RopeFreq& rf, int j) {
+  return rp.inv_freq ? rp.inv_freq[j] : rf.f[j];
 }
 
 // Position rotating frequency index j (0 <= j < rot/2). Selects on values

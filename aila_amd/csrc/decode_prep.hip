@@ -53,7 +53,7 @@ __device__ __forceinline__ void norm_head_to_lds(const bf16* __restrict__ x, con
 // stream).
 template <int D>
 __device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restrict__ y, int rot, RowPos rp,
-                                              float theta, const float* __restrict__ inv_freq) {
+                                              const RopePos& rpos, const RopeFreq& rf) {
   constexpr int E = D / 64;
   const int lane = threadIdx.x & 63;
   const int half = rot / 2;
@@ -63,7 +63,7 @@ __device__ __forceinline__ void rope_from_lds(const float* s_row, bf16* __restri
     float r = s_row[d];
     if (d < rot) {
       const int dd = d < half ? d : d - half;                 // frequency index
-      const float freq = inv_freq ? inv_freq[dd] : 1.0f / powf(theta, (2.0f * dd) / static_cast<float>(rot));
+      const float freq = rope_inv_freq(rpos, rf, dd);
       const float ang = rope_freq_pos(rp, dd) * freq;
       const float c = cosf(ang), s = sinf(ang);
       r = d < half ? s_row[d] * c - s_row[d + half] * s : s_row[d] * c + s_row[d - half] * s;
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(
     const bf16* __restrict__ q_in, int q_in_stride, bf16* __restrict__ q_out, bf16* __restrict__ gate_out,
     bf16* __restrict__ k, const bf16* __restrict__ v, const bf16* __restrict__ qn_w,
     const bf16* __restrict__ kn_w, bf16* __restrict__ k_cache, bf16* __restrict__ v_cache, int Hq, int Hkv,
-    int max_seq, int rot, float theta, float eps, int pos, const int* __restrict__ positions, RopePos ropep) {
+    int max_seq, int rot, RopeFreq rf, float eps, int pos, const int* __restrict__ positions, RopePos ropep) {
   __shared__ float s_row[D];
   const int hh = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
@@ -92,14 +92,14 @@ __global__ __launch_bounds__(64) void decode_prep_kernel(
     }
     norm_head_to_lds<D>(src, qn_w, eps, s_row);
     __syncthreads();
-    rope_from_lds<D>(s_row, dst, rot, rp, theta, ropep.inv_freq);
+    rope_from_lds<D>(s_row, dst, rot, rp, ropep, rf);
     return;
   }
   const int h = hh - Hq;
   bf16* kr = k + (static_cast<size_t>(b) * Hkv + h) * D;
   norm_head_to_lds<D>(kr, kn_w, eps, s_row);
   __syncthreads();
-  rope_from_lds<D>(s_row, kr, rot, rp, theta, ropep.inv_freq);
+  rope_from_lds<D>(s_row, kr, rot, rp, ropep, rf);
   if (k_cache && p >= 0 && p < max_seq) {
     // each lane re-reads only the elements it wrote itself
     const size_t row = ((static_cast<size_t>(b) * Hkv + h) * max_seq + p) * D;
@@ -129,14 +129,14 @@ __global__ __launch_bounds__(64) void head_rms_norm_kernel(bf16* __restrict__ x,
 // (head, token).
 template <int D>
 __global__ __launch_bounds__(64) void rope_kernel(bf16* __restrict__ q, bf16* __restrict__ k, int Hq, int Hkv,
-                                                 int start_pos, int rot, float theta, RopePos ropep) {
+                                                 int start_pos, int rot, RopeFreq rf, RopePos ropep) {
   __shared__ float s_row[D];
   const int hh = blockIdx.x, s = blockIdx.y;
   bf16* row = hh < Hq ? q + (static_cast<size_t>(s) * Hq + hh) * D : k + (static_cast<size_t>(s) * Hkv + hh - Hq) * D;
   const int lane = threadIdx.x;
   for (int d = lane; d < D; d += 64) s_row[d] = bf2f(row[d]);
   __syncthreads();
-  rope_from_lds<D>(s_row, row, rot, rope_row_pos(ropep, 0, start_pos + s), theta, ropep.inv_freq);
+  rope_from_lds<D>(s_row, row, rot, rope_row_pos(ropep, 0, start_pos + s), ropep, rf);
 }
 
 // o = in * sigmoid(g), 8 elements per thread where n allows.
@@ -209,7 +209,8 @@ extern "C" int aila_hip_decode_prepare_qkv(const void* q_in, int packed_gate, vo
                        packed_gate ? static_cast<bf16*>(gate_out) : nullptr, static_cast<bf16*>(k),
                        static_cast<const bf16*>(v), static_cast<const bf16*>(q_norm_w),
                        static_cast<const bf16*>(k_norm_w), static_cast<bf16*>(k_cache),
-                       static_cast<bf16*>(v_cache), Hq, Hkv, max_seq, rot, theta, eps, pos, positions, rpd);
+                       static_cast<bf16*>(v_cache), Hq, Hkv, max_seq, rot, rope_freq_table(theta, rot), eps, pos,
+                       positions, rpd);
     return check_launch("decode_prepare_qkv");
   });
 }
@@ -245,7 +246,7 @@ extern "C" int aila_hip_apply_rope(void* q, void* k, int S, int start_pos, int H
   return with_d(D, "apply_rope", [&](auto dc) {
     constexpr int DD = decltype(dc)::value;
     hipLaunchKernelGGL((rope_kernel<DD>), dim3(Hq + Hkv, S), dim3(64), 0, st, static_cast<bf16*>(q),
-                       static_cast<bf16*>(k), Hq, Hkv, start_pos, rot, theta, rpd);
+                       static_cast<bf16*>(k), Hq, Hkv, start_pos, rot, rope_freq_table(theta, rot), rpd);
     return check_launch("apply_rope");
   });
 }

@@ -62,8 +62,9 @@ struct PrepArgs {
   bf16* gate_out;        // [B, Hq, D] (packed only) or null
   int apply_gate;        // packed only: out *= sigmoid(gate) instead of copying the gate out
   int rot;               // rotary dims, even, in [2, D]
-  float theta, eps;
+  float eps;
   RopePos rope;          // rotary positions (zero: the cache row)
+  RopeFreq freq;         // inverse frequencies of the rotary pairs
 };
 
 // Paged KV cache: the rows of sequence b live in fixed-size pages of a
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(kThreads) void gqa_decode_split_kernel(
     const int half = pa.rot / 2;
     const RowPos rp = rope_row_pos(pa.rope, b, len - 1);
     for (int j = threadIdx.x; j < half; j += kThreads) {
-      const float freq = rope_inv_freq(pa.rope, j, pa.rot, pa.theta);
+      const float freq = rope_inv_freq(pa.rope, pa.freq, j);
       const float ang = rope_freq_pos(rp, j) * freq;
       s_tab[2 * j] = cosf(ang);
       s_tab[2 * j + 1] = sinf(ang);
@@ -986,7 +987,7 @@ extern "C" int aila_hip_gqa_decode_prepare_append(const void* q_in, int packed_g
   pa.gate_out = packed_gate == 1 ? static_cast<bf16*>(gate_out) : nullptr;
   pa.apply_gate = packed_gate == 2;
   pa.rot = rot;
-  pa.theta = theta;
+  pa.freq = rope_freq_table(theta, rot);
   pa.eps = eps;
   if (int rc = load_rope_pos(rope_pos, &pa.rope, "gqa_decode_prepare_append")) return rc;
   return gqa_decode_impl(q_in, k_cache, v_cache, out, workspace, workspace_bytes, B, Hq, Hkv, D, max_seq, pos + 1,

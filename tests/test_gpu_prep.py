@@ -495,3 +495,76 @@ def test_fused_decode_first_chunk_waits_for_its_dma():
                                            err_msg=f"launch {rep} sequence {b} split {i} max")
                 err = np.abs(r[:, 16:] / r[:, 1:2] - want).max() / np.abs(want).max()
                 assert err <= 2e-2, f"launch {rep} sequence {b} split {i}: {err}"
+
+
+def _close(got, want):
+    """Rotations at long positions: within 1e-3 and nearly every element
+    bit-equal (the frequencies, angles and products are the oracle's floats;
+    cos/sin may differ in the last bit)."""
+    assert _relerr(got, want) <= 1e-3
+    assert np.mean(got == want) >= 0.99
+
+
+@pytest.mark.parametrize("D,rot,theta", [(128, 128, 1e6), (256, 64, 1e7), (64, 64, 1e4)])
+def test_rope_at_long_positions(D, rot, theta):
+    """Positions up to 2^20 (ElementwiseOps.cpp:80-83: angle = position *
+    1/pow(theta, 2d/rot)). The inverse frequencies are the correctly rounded
+    floats of that formula; with the device powf (not correctly rounded) a
+    frequency one ulp off turned the angle by position * ulp, ~3e-2 relative
+    error at position 1M."""
+    import torch
+    import aila_amd
+    B, Hq, Hkv = 3, 8, 2
+    pos = np.array([65535, 262143, 1048575], np.int32)
+    q = dg.normal_bf16(740 + D, 0, (B, Hq, D))
+    k = dg.normal_bf16(740 + D, 1, (B, Hkv, D))
+    v = dg.normal_bf16(740 + D, 2, (B, Hkv, D))
+    q_d, k_d = _t(q), _t(k)
+    aila_amd.decode_prepare_qkv(q_d, k_d, _t(v), positions=_t(pos), rotary_dim=rot, theta=theta)
+    torch.cuda.synchronize()
+    qo, _, ko = oracle.decode_prepare(q, k, v, None, None, None, None, pos, B, Hq, Hkv, D, 0, rot, theta, 1e-6)
+    _close(_np(q_d), qo)
+    _close(_np(k_d), ko)
+    # prefill rows at the same range of positions
+    S, start = 6, 1048570
+    qs = dg.normal_bf16(741 + D, 0, (S, Hq, D))
+    ks = dg.normal_bf16(741 + D, 1, (S, Hkv, D))
+    qsd, ksd = _t(qs), _t(ks)
+    aila_amd.apply_rope(qsd, ksd, start_pos=start, rotary_dim=rot, theta=theta)
+    torch.cuda.synchronize()
+    qw, kw = oracle.apply_rope(qs.reshape(S, -1), ks.reshape(S, -1), S, start, Hq, Hkv, D, rot, theta)
+    _close(_np(qsd), qw.reshape(S, Hq, D))
+    _close(_np(ksd), kw.reshape(S, Hkv, D))
+
+
+def test_fused_prepare_append_decode_long_position():
+    """The one-launch prep + append + decode at cache row 262143 (a 256k
+    context, Qwen3.5 attention shape): the appended, rotated k row against
+    the oracle's prep, and the attention over all 262144 rows."""
+    import torch
+    import aila_amd
+    B, Hq, Hkv, D, rot, theta, eps = 1, 4, 1, 256, 64, 1e7, 1e-6
+    pos = np.array([262143], np.int32)
+    max_seq = 262144
+    seed = 750
+    print(f"fused prep long position pos={pos[0]} max_seq={max_seq}", flush=True)
+    q = dg.normal_bf16(seed, 0, (B, Hq, 2 * D), std=2.0)
+    k = dg.normal_bf16(seed, 1, (B, Hkv, D), std=2.0)
+    v = dg.normal_bf16(seed, 2, (B, Hkv, D))
+    qw = dg.normal_bf16(seed, 3, (D,))
+    kw = dg.normal_bf16(seed, 4, (D,))
+    kc = dg.normal_bf16(seed, 5, (B, Hkv, max_seq, D))
+    vc = dg.normal_bf16(seed, 6, (B, Hkv, max_seq, D))
+    kc_d, vc_d = _t(kc), _t(vc)
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    out, gate = aila_amd.gqa_decode_prepare_append(
+        _t(q), _t(k), _t(v), kc_d, vc_d, int(pos[0]), q_norm_w=_t(qw), k_norm_w=_t(kw), rotary_dim=rot,
+        theta=theta, eps=eps, packed_gate=True, positions=_t(pos), workspace=ws)
+    torch.cuda.synchronize()
+    qo, gw, ko = oracle.decode_prepare(q, k, v, qw, kw, kc, vc, pos, B, Hq, Hkv, D, max_seq, rot, theta, eps,
+                                       packed=True)
+    _close(_np(kc_d)[0, :, pos[0]], ko[0])
+    assert np.array_equal(_np(vc_d)[0, :, pos[0]], v[0])
+    assert np.array_equal(_np(gate), gw)
+    want = oracle.attention_decode_baseline(qo, kc, vc, 1, Hq, Hkv, D, max_seq, int(pos[0]) + 1)[0]
+    assert _relerr(_np(out)[0], want) <= TOL
