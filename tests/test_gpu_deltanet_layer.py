@@ -167,7 +167,8 @@ def _slow_decay(x):
 @pytest.mark.parametrize("B,T,Hk,Hv,head0,slow", [(2, 200, 2, 4, 1, False), (1, 1024, 16, 32, 0, False),
                                                   (1, 1024, 2, 4, 2, True), (3, 64, 1, 1, 0, False),
                                                   (1, 5, 2, 2, 2, False), (2, 1, 2, 4, 1, False),
-                                                  (1, 2, 1, 2, 2, False)])   # T < 3: the ring keeps old rows
+                                                  (1, 2, 1, 2, 2, False),    # T < 3: the ring keeps old rows
+                                                  (1, 32768, 1, 2, 1, True)])  # 512 chunks, long-memory heads
 def test_layer_prefill_matches_oracle(B, T, Hk, Hv, head0, slow):
     import torch
     import aila_amd
