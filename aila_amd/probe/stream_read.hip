@@ -1,6 +1,6 @@
 // Ceiling probes for the benchmark: the HBM read rate this chip reaches
-// over the GQA decode's exact K/V layout, and the dense bf16 MFMA rate it
-// sustains, reported beside the decode's and the prefill's rooflines as the
+// over the GQA decode's exact K/V layout, the in-place read + write rate over
+// a DeltaNet state, and the dense bf16 MFMA rate it sustains, reported beside the decode's and the prefill's rooflines as the
 // achievable ceilings. Measurement only: they are built into their own
 // library (libaila_probe.so), which the benchmark loads and the product
 // never does.
@@ -53,6 +53,26 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const unsigned ch
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// In-place read + write: every 16-byte chunk of a buffer is read and
+// written back (nontemporal both ways, sixteen in flight per thread), the
+// traffic of a DeltaNet decode step over its fp32 state with no
+// arithmetic. The value written is the value read XOR `key`, a kernel
+// argument the host passes as 0: the buffer keeps its contents, and the
+// compiler cannot drop the store (or with it the load) as a copy of a
+// location onto itself.
+__global__ __launch_bounds__(kThreads) void stream_rw_kernel(u32x4* __restrict__ p, size_t n16, unsigned key) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * kThreads;
+  size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  for (; i + (kUnroll - 1) * stride < n16; i += kUnroll * stride) {
+    u32x4 x[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) x[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(x[u] ^ key, p + i + u * stride);
+  }
+  for (; i < n16; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(p + i) ^ key, p + i);
+}
+
 // Dense MFMA: every wave issues `iters` rounds of 16 independent
 // v_mfma_f32_16x16x32_bf16 (16,384 FLOP each) on register operands; the
 // accumulators are folded and stored only if they equal a constant no run
@@ -92,6 +112,17 @@ extern "C" int aila_probe_stream_read(const void* k_cache, const void* v_cache, 
   hipLaunchKernelGGL(stream_read_kernel, dim3(nsplit, Hkv, B), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const unsigned char*>(k_cache),
                      static_cast<const unsigned char*>(v_cache), Hkv, max_seq, len, D, sink);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Reads and writes back `bytes` (a multiple of 16) of `buf` in place, with
+// `blocks` workgroups of 256 threads. Returns a hipError_t.
+extern "C" int aila_probe_stream_rw(void* buf, size_t bytes, int blocks, void* stream) {
+  if (!buf || bytes % 16 != 0 || blocks <= 0 || reinterpret_cast<uintptr_t>(buf) % 16 != 0)
+    return static_cast<int>(hipErrorInvalidValue);
+  if (bytes == 0) return 0;
+  hipLaunchKernelGGL(stream_rw_kernel, dim3(blocks), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<u32x4*>(buf), bytes / 16, 0u);
   return static_cast<int>(hipGetLastError());
 }
 
