@@ -248,3 +248,35 @@ def test_decode_append_uniform_position():
     vc[:, :, p] = vn
     want = dg.bf16_to_f32(oracle.attention_decode_baseline(q, kc, vc, B, Hq, Hkv, D, max_seq, p + 1))
     assert _relerr(dg.bf16_to_f32(_np_bf16(out)), want) <= ATTN_TOL
+
+
+def test_decode_cache_beyond_2g_elements():
+    """A 1M-row context in a batched cache of 4.5 GB per tensor: the second
+    sequence's rows sit past element 2^31 of the cache (and its last KV head
+    past 2^32 bytes), so any 32-bit index or byte offset in the kernels would
+    read the wrong rows. Split-K and single-pass against the oracle."""
+    import torch
+    import aila_amd
+    B, Hq, Hkv, D = 2, 16, 4, 256
+    max_seq = 1_100_000
+    lens = [1000, 1_048_581]
+    print(f"decode over a {max_seq}-row batched cache, lens={lens}", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 60)
+    kc = torch.randn((B, Hkv, max_seq, D), generator=g, dtype=torch.bfloat16, device="cuda")
+    vc = torch.randn((B, Hkv, max_seq, D), generator=g, dtype=torch.bfloat16, device="cuda")
+    q = torch.randn((B, Hq, D), generator=g, dtype=torch.bfloat16, device="cuda")
+    sl = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    ws = torch.empty(aila_amd.gqa_decode_workspace_size(B, Hq, D), dtype=torch.uint8, device="cuda")
+    outs = [aila_amd.gqa_decode(q, kc, vc, max_seq, workspace=w, seq_lens=sl) for w in (ws, None)]
+    torch.cuda.synchronize()
+    qh = _np_bf16(q)
+    for b, L in enumerate(lens):
+        kb = _np_bf16(kc[b:b + 1, :, :L].contiguous())
+        vb = _np_bf16(vc[b:b + 1, :, :L].contiguous())
+        want = dg.bf16_to_f32(oracle.attention_decode_baseline(qh[b:b + 1], kb, vb, 1, Hq, Hkv, D, L, L))[0]
+        for i, out in enumerate(outs):
+            got = dg.bf16_to_f32(_np_bf16(out)[b])
+            assert np.isfinite(got).all()
+            assert _relerr(got, want) <= ATTN_TOL, (b, L, "split" if i == 0 else "single")
+        del kb, vb

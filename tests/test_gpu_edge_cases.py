@@ -264,3 +264,34 @@ def test_attention_with_large_logits(std):
     want = dg.bf16_to_f32(oracle.attention_prefill_cached(q, kc, vc, S, start, Hq, Hkv, D, ms))
     rows = np.max(np.abs(out - want), axis=1) / np.max(np.abs(want), axis=1)
     assert np.max(rows) <= ATTN_TOL
+
+
+def test_decode_state_beyond_2g_elements():
+    """A batch of 4100 sequences of the config-5 DeltaNet shape: an 8.6 GB
+    fp32 state, so the last sequences' heads sit past element 2^31 (and byte
+    2^33); one step checked against the oracle at the first and last
+    sequence."""
+    import torch
+    import aila_amd
+    B, Hk, Hv, d = 4100, 16, 32, 128
+    print(f"deltanet decode B={B} (state {B * Hv * d * d * 4 / 2**30:.1f} GiB)", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xA11A + 61)
+    st = torch.empty((B, Hv, d, d), dtype=torch.float32, device="cuda").normal_(0, 0.02, generator=g)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    q = torch.randn((B, Hk, d), generator=g, **bf)
+    k = torch.randn((B, Hk, d), generator=g, **bf)
+    v = torch.randn((B, Hv, d), generator=g, **bf)
+    a = torch.randn((B, Hv), generator=g, **bf)
+    b = torch.randn((B, Hv), generator=g, **bf)
+    picks = (0, B - 1)
+    before = {i: st[i:i + 1].cpu().numpy() for i in picks}
+    out = aila_amd.deltanet_decode(q, k, v, a, b, st)
+    torch.cuda.synchronize()
+    for i in picks:
+        sl = slice(i, i + 1)
+        _, want_o, want_S = oracle.deltanet_recurrent(_np(q[sl])[:, None], _np(k[sl])[:, None], _np(v[sl])[:, None],
+                                                      _np(a[sl])[:, None], _np(b[sl])[:, None], before[i], 1, 1,
+                                                      Hk, Hv, d, d)
+        assert _relerr(st[sl].cpu().numpy(), want_S) <= STATE_TOL, i
+        assert _relerr(dg.bf16_to_f32(_np(out[sl])), dg.bf16_to_f32(want_o).reshape(1, Hv, d)) <= ATTN_TOL, i
