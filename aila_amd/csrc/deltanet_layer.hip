@@ -493,14 +493,36 @@ extern "C" int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride, 
                    aligned(z, 16) && z_stride % 8 == 0 && aligned(norm_w, 16) && aligned(state, 16) &&
                    aligned(out, 16),
                "deltanet_layer_prefill: misaligned qkv/conv_w/conv_state/z/norm_w/state/out or odd strides");
-  // a sequence's fused rows are read through one buffer resource (32-bit range)
-  AILA_REQUIRE(static_cast<long>(T) * qkv_stride * 2 < (1L << 31),
-               "deltanet_layer_prefill: T * qkv_stride = %ld elements exceed one 2 GiB range per sequence",
-               static_cast<long>(T) * qkv_stride);
   const size_t need = layer_ws_bytes(B, T, Hv);
   if (!workspace || workspace_bytes < need)
     return set_error(AILA_HIP_EWORKSPACE, "deltanet_layer_prefill: workspace %zu < %zu bytes", workspace_bytes,
                      need);
+  // A sequence's fused rows are read through one buffer resource, a 2 GiB
+  // byte range. Longer inputs run per sequence in consecutive segments of
+  // whole chunks, each a call of its own: the state and the conv ring pass
+  // from one segment to the next as between two calls (ring head advanced
+  // by the segment's tokens), and the chunks are the ones a single call
+  // would form, so the results are the same.
+  const long max_rows = ((1L << 31) - 1) / (static_cast<long>(qkv_stride) * 2) / 64 * 64;
+  if (T > max_rows) {
+    AILA_REQUIRE(max_rows >= 64, "deltanet_layer_prefill: qkv_stride=%d leaves no 64-row chunk in 2 GiB",
+                 qkv_stride);
+    for (int bb = 0; bb < B; ++bb) {
+      for (long t0 = 0; t0 < T; t0 += max_rows) {
+        const int ts = static_cast<int>(std::min<long>(max_rows, T - t0));
+        const size_t row = static_cast<size_t>(bb) * T + t0;
+        const int rc = aila_hip_deltanet_layer_prefill(
+            static_cast<const bf16*>(qkv) + row * qkv_stride, qkv_stride, static_cast<const bf16*>(z) + row * z_stride,
+            z_stride, static_cast<const bf16*>(a) + row * ab_stride, static_cast<const bf16*>(b) + row * ab_stride,
+            ab_stride, conv_w, conv_state + static_cast<size_t>(bb) * kRows * ch,
+            static_cast<int>((conv_head + t0) % kRows), dt_bias, A_log, norm_w,
+            state + static_cast<size_t>(bb) * Hv * kD * kD, static_cast<bf16*>(out) + row * Hv * kD, workspace,
+            workspace_bytes, 1, ts, Hk, Hv, dk, dv, conv_kernel, eps, scale, stream);
+        if (rc != AILA_HIP_OK) return rc;
+      }
+    }
+    return AILA_HIP_OK;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int head = ((conv_head % kRows) + kRows) % kRows;
   const ConvIn cv{static_cast<const bf16*>(qkv), qkv_stride, static_cast<const bf16*>(conv_w), conv_state, head, ch};

@@ -160,14 +160,15 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   };
   auto qb_of = [&](int it) __attribute__((always_inline)) { return (grp == 0 && it < nl) ? ql : qh; };
   const int kv_len = start_pos + S;
-  const bf16* Kh = k + kvh * kv_head_stride;
-  const bf16* Vh = v + kvh * kv_head_stride;
+  const bf16* Kh = k + static_cast<size_t>(kvh) * kv_head_stride;
+  const bf16* Vh = v + static_cast<size_t>(kvh) * kv_head_stride;
 
   // ---- K/V block -> LDS by DMA (wave-contiguous KiB per instruction) ------
   // Buffer loads straight into LDS. The buffer resource of a block starts at
-  // its first key row and ends at the last valid row (kv_len), so rows past
-  // a ragged end read as zeros (those keys are causally masked) and every
-  // lane's byte offset is a constant of the kernel.
+  // its first key row and ends at its last row or the last valid row
+  // (kv_len), whichever comes first, so rows past a ragged end read as zeros
+  // (those keys are causally masked), every lane's byte offset is a constant
+  // of the kernel, and the 32-bit range never spans more than one block.
   // (Fixed extent: an array sized by C::LOADS and captured by the lambdas
   // below makes the host pass drop the kernel's launch stub.)
   static_assert(C::LOADS <= 8, "dma_off extent");
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   auto issue_tile = [&](unsigned char* tile, const bf16* base, const int* off, int kb) __attribute__((always_inline)) {
     const int key0 = kb * BN;
     const u32x4 src = buffer_rsrc(base + static_cast<size_t>(key0) * kv_row_stride,
-                                  (kv_len - key0) * kv_row_stride * 2);
+                                  min(kv_len - key0, BN) * kv_row_stride * 2);
 #pragma unroll
     for (int i = 0; i < C::LOADS; ++i) dma16_to_lds(src, off[i], tile + (i * kWaves + wave) * 64 * 16);
   };
@@ -209,10 +210,13 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
   // The heavy block's Q operands of this wave, in [qt][ks][lane] order.
   unsigned char* my_qh = sQh + wave * (C::QT * C::KS * 1024);
   auto stage_segment_q = [&](int qb) __attribute__((always_inline)) {
+    // a range over this block's rows only (rows past S clamp to the last)
+    const int row0 = qb * C::BM;
+    const u32x4 src = buffer_rsrc(q + static_cast<size_t>(row0) * q_row_stride + h * D,
+                                  (min(row0 + C::BM, S) - 1 - row0) * q_row_stride * 2 + D * 2);
 #pragma unroll
     for (int qt = 0; qt < C::QT; ++qt) {
-      const int row = min(qb * C::BM + wave * RPW + qt * 16 + m16, S - 1);
-      const u32x4 src = buffer_rsrc(q + h * D, (S - 1) * q_row_stride * 2 + D * 2);
+      const int row = min(row0 + wave * RPW + qt * 16 + m16, S - 1) - row0;
 #pragma unroll
       for (int ks = 0; ks < C::KS; ++ks)
         dma16_to_lds(src, (row * q_row_stride + g4 * 8 + ks * 32) * 2, my_qh + (qt * C::KS + ks) * 1024);
@@ -762,9 +766,6 @@ extern "C" int aila_hip_gqa_prefill(const void* q, const void* k, const void* v,
   AILA_REQUIRE(S > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq <= 65535,
                "gqa_prefill: bad shape (S=%d Hq=%d Hkv=%d)", S, Hq, Hkv);
   AILA_REQUIRE((k_cache == nullptr) == (v_cache == nullptr), "gqa_prefill: pass both caches or neither");
-  // q and the chunk's K/V are addressed through 32-bit buffer ranges
-  AILA_REQUIRE(static_cast<long>(S) * Hq * D * 2 < (1L << 31),
-               "gqa_prefill: S * Hq * D = %ld elements exceed one 2 GiB range", static_cast<long>(S) * Hq * D);
   if (k_cache) {
     AILA_REQUIRE(cache_pos >= 0 && static_cast<long>(cache_pos) + S <= max_seq,
                  "gqa_prefill: cache rows [%d, %d) exceed max_seq=%d", cache_pos, cache_pos + S, max_seq);
@@ -791,8 +792,9 @@ extern "C" int aila_hip_gqa_prefill_cached_ws(const void* q, const void* k_cache
                "gqa_prefill_cached: bad shape (S=%d start_pos=%d Hq=%d Hkv=%d)", S, start_pos, Hq, Hkv);
   AILA_REQUIRE(static_cast<long>(start_pos) + S <= max_seq,
                "gqa_prefill_cached: start_pos + S = %ld > max_seq=%d", static_cast<long>(start_pos) + S, max_seq);
-  AILA_REQUIRE(static_cast<long>(S) * Hq * D * 2 < (1L << 31) && static_cast<long>(max_seq) * D * 2 < (1L << 31),
-               "gqa_prefill_cached: q or a cache head exceeds one 2 GiB range");
+  // a cache head's extent (max_seq * D) is passed to the kernel as an int
+  AILA_REQUIRE(static_cast<long>(max_seq) * D * 2 < (1L << 31),
+               "gqa_prefill_cached: a cache head (max_seq=%d, D=%d) exceeds 2 GiB", max_seq, D);
   AILA_REQUIRE(workspace == nullptr || reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                "gqa_prefill_cached: workspace not 16-byte aligned");
   int nz = 1;

@@ -370,7 +370,9 @@ size_t aila_hip_deltanet_layer_prefill_workspace_size(int B, int T, int Hk,
  * aila_hip_deltanet_prefill; the last pass applies the gated RMSNorm and
  * rewrites the ring. out [B, T, Hv*dv] bf16. Chunked path: dk = dv = 128,
  * conv kernel 4, Hv % Hk == 0; qkv 8-byte aligned with qkv_stride a
- * multiple of 4 and T*qkv_stride*2 < 2^31. Other shapes (dk, dv <= 256,
+ * multiple of 4 (a sequence whose rows span 2 GiB or more runs as
+ * consecutive segments of whole 64-token chunks inside the call, with the
+ * same results). Other shapes (dk, dv <= 256,
  * conv kernel 1..16, any head counts) run the general-shape kernel token by
  * token, as the reference's batched prefill does; no workspace. */
 int aila_hip_deltanet_layer_prefill(const void* qkv, int qkv_stride,

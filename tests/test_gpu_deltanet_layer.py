@@ -242,3 +242,36 @@ def test_layer_prefill_fused_rows_then_decode():
     assert _rel(_np(st), want_S) <= STATE_TOL
     assert _rel(dg.bf16_to_f32(got), dg.bf16_to_f32(want_out)) <= OUT_TOL
     assert np.array_equal(_np(cs), want_cs)
+
+
+def test_layer_prefill_rows_past_one_2gib_range():
+    """Fused rows padded to 64Ki elements (128 KiB a row) over 20000 tokens:
+    2.6 GB of rows per sequence, more than the 2 GiB one buffer range
+    covers, so the entry point runs each sequence in segments of whole
+    chunks (16320 tokens, then the rest), the state and the conv ring passed
+    between them. Bit for bit against the same rows packed densely (one
+    call per the whole sequence), and against the oracle."""
+    import torch
+    import aila_amd
+    B, T, Hk, Hv, head0 = 2, 20000, 1, 2, 1
+    x = _inputs(990, B, T, Hk, Hv)
+    ch = x["qkv"].shape[2]
+    pad = 65536
+    print(f"layer prefill over padded rows B={B} T={T} row={pad} elements", flush=True)
+    big = torch.zeros((B, T, pad), dtype=torch.bfloat16, device="cuda")
+    big[:, :, :ch] = _t(x["qkv"])
+    w, nw, dtb, alog = _t(x["conv_w"]), _t(x["norm_w"]), _t(x["dt_bias"]), _t(x["A_log"])
+    z, a, b = _t(x["z"]), _t(x["a"]), _t(x["b"])
+    res = []
+    for qkv in (big[:, :, :ch], _t(x["qkv"])):
+        st, cs = _t(x["state"]), _t(x["conv_state"])
+        out = aila_amd.deltanet_layer_prefill(qkv, z, a, b, w, cs, head0, nw, st, Hk, dt_bias=dtb, A_log=alog)
+        torch.cuda.synchronize()
+        res.append((_np(out), _np(st), _np(cs)))
+    del big
+    for got, dense in zip(res[0], res[1]):
+        assert np.array_equal(got, dense)
+    want_out, want_S, want_cs = _oracle(x, B, T, Hk, Hv, head0)
+    assert _rel(res[0][1], want_S) <= STATE_TOL
+    assert _rel(dg.bf16_to_f32(res[0][0]), dg.bf16_to_f32(want_out)) <= OUT_TOL
+    assert np.array_equal(res[0][2], want_cs)

@@ -267,10 +267,12 @@ def _rows_against_decode(q, kc, vc, got, rows, base, Hq, Hkv, D, max_seq):
 
 
 @pytest.mark.parametrize("S,Hq,Hkv,D", [(16384, 4, 1, 128), (8192, 4, 2, 256), (12000, 2, 1, 64),
-                                         (65536, 2, 1, 128), (131072, 2, 1, 64)])
+                                         (65536, 2, 1, 128), (131072, 2, 1, 64),
+                                         (262144, 16, 2, 256)])   # q of exactly 2 GiB
 def test_prefill_long_prompt_rows_match_decode(S, Hq, Hkv, D):
-    """Prompts of 8k-128k tokens (the naive oracle prefill would take minutes
-    to hours at these sizes): sampled rows against the oracle's decode over the same
+    """Prompts of 8k-256k tokens (the naive oracle prefill would take minutes
+    to days at these sizes; the last is a full 262144-token Qwen3.5 context
+    whose q spans 2 GiB): sampled rows against the oracle's decode over the same
     rows, every output finite, and the fused cache write bit-exact."""
     import torch
     import aila_amd
