@@ -131,7 +131,7 @@ template <int D>
 __global__ __launch_bounds__(64) void rope_kernel(bf16* __restrict__ q, bf16* __restrict__ k, int Hq, int Hkv,
                                                  int start_pos, int rot, RopeFreq rf, RopePos ropep) {
   __shared__ float s_row[D];
-  const int hh = blockIdx.x, s = blockIdx.y;
+  const int s = blockIdx.x, hh = blockIdx.y;   // tokens on x: no 65535 cap on S
   bf16* row = hh < Hq ? q + (static_cast<size_t>(s) * Hq + hh) * D : k + (static_cast<size_t>(s) * Hkv + hh - Hq) * D;
   const int lane = threadIdx.x;
   for (int d = lane; d < D; d += 64) s_row[d] = bf2f(row[d]);
@@ -238,14 +238,14 @@ extern "C" int aila_hip_apply_rope(void* q, void* k, int S, int start_pos, int H
   AILA_REQUIRE(q && k, "apply_rope: null pointer");
   RopePos rpd;
   if (int rc = load_rope_pos(rope_pos, &rpd, "apply_rope")) return rc;
-  AILA_REQUIRE(S >= 0 && S <= 65535 && start_pos >= 0 && Hq > 0 && Hkv > 0 && Hkv <= Hq && theta > 0.f,
+  AILA_REQUIRE(S >= 0 && start_pos >= 0 && Hq > 0 && Hkv > 0 && Hkv <= Hq && Hq + Hkv <= 65535 && theta > 0.f,
                "apply_rope: bad shape (S=%d start_pos=%d Hq=%d Hkv=%d)", S, start_pos, Hq, Hkv);
   if (S == 0) return AILA_HIP_OK;
   const int rot = clamp_rot(D, rotary_dim);
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_d(D, "apply_rope", [&](auto dc) {
     constexpr int DD = decltype(dc)::value;
-    hipLaunchKernelGGL((rope_kernel<DD>), dim3(Hq + Hkv, S), dim3(64), 0, st, static_cast<bf16*>(q),
+    hipLaunchKernelGGL((rope_kernel<DD>), dim3(S, Hq + Hkv), dim3(64), 0, st, static_cast<bf16*>(q),
                        static_cast<bf16*>(k), Hq, Hkv, start_pos, rot, rope_freq_table(theta, rot), rpd);
     return check_launch("apply_rope");
   });

@@ -498,10 +498,12 @@ def test_fused_decode_first_chunk_waits_for_its_dma():
 
 
 def _close(got, want):
-    """Rotations at long positions: within 1e-3 and nearly every element
-    bit-equal (the frequencies, angles and products are the oracle's floats;
-    cos/sin may differ in the last bit)."""
-    assert _relerr(got, want) <= 1e-3
+    """Rotations at long positions: at least 99% of the elements bit-equal
+    (the frequencies, angles and products are the oracle's floats; cos/sin
+    may differ in the last bit and flip a rounding) and the rest within the
+    path's tolerance. With the device powf's frequencies 1.3-9% of the
+    elements differed at position 1048575."""
+    assert _relerr(got, want) <= TOL
     assert np.mean(got == want) >= 0.99
 
 
@@ -568,3 +570,19 @@ def test_fused_prepare_append_decode_long_position():
     assert np.array_equal(_np(gate), gw)
     want = oracle.attention_decode_baseline(qo, kc, vc, 1, Hq, Hkv, D, max_seq, int(pos[0]) + 1)[0]
     assert _relerr(_np(out)[0], want) <= TOL
+
+
+def test_apply_rope_prompt_past_65535_tokens():
+    """A 100000-token prompt through apply_rope (tokens on the grid's x axis,
+    so no 65535-token cap): every row against the oracle."""
+    import torch
+    import aila_amd
+    S, Hq, Hkv, D, rot, start = 100000, 2, 1, 64, 64, 7
+    q = dg.normal_bf16(745, 0, (S, Hq, D))
+    k = dg.normal_bf16(745, 1, (S, Hkv, D))
+    qd, kd = _t(q), _t(k)
+    aila_amd.apply_rope(qd, kd, start_pos=start, rotary_dim=rot, theta=1e6)
+    torch.cuda.synchronize()
+    qw, kw = oracle.apply_rope(q.reshape(S, -1), k.reshape(S, -1), S, start, Hq, Hkv, D, rot, 1e6)
+    _close(_np(qd), qw.reshape(S, Hq, D))
+    _close(_np(kd), kw.reshape(S, Hkv, D))
