@@ -54,6 +54,7 @@ def _kept(L, window, start, sink):
     (3, 8, 2, 128, 4096, 4000, [4000, 1800, 700], 512, 1024, 37, True),   # device lengths, one below start
     (1, 16, 8, 128, 2048, 2000, None, 100, 512, 0, True),      # tail only, ragged window
     (2, 8, 8, 64, 2048, 1999, [1999, 1500], 300, 512, 1300, True),  # sink and tail meet for one sequence
+    (1, 16, 4, 256, 131136, 131072, None, 4096, -1, 4, True),  # a 4k window at the end of a 128k context
 ])
 def test_decode_window(B, Hq, Hkv, D, max_seq, L, lens, window, start, sink, split):
     import torch
