@@ -322,6 +322,29 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
             if (kt * 16 + j > rel) st[kt][qt][j] = -INFINITY;
       }
     }
+    // P at the running maxima, issued before the block's maxima are known;
+    // the lazy rescale leaves a maximum in place unless the block exceeds it
+    // by 2^8, so these are the final P of every row but where one grows (or
+    // at a row's first block), when the wave recomputes its P below.
+    auto exp_pass = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int qt = 0; qt < C::QT; ++qt) {
+        const float nm = (m_run[qt] == -INFINITY) ? 0.f : -m_run[qt];
+#pragma unroll
+        for (int s2 = 0; s2 < C::PS; ++s2) {
+          float p[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
+            p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
+          }
+          const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                           pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
+          pb[s2][qt] = as_bf16x8(w);
+        }
+      }
+    };
+    exp_pass();
     float alpha[C::QT];
     bool any_rescale = false;
 #pragma unroll
@@ -332,36 +355,15 @@ __global__ __launch_bounds__(2 * kThreads, 1) void gqa_prefill_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) mx = fmaxf(mx, st[kt][qt][j]);
       mx = xrow4_max(mx) * scale_log2;
-      // Lazy rescaling: the reference max only moves when the block max
-      // exceeds it by more than 2^8 (p <= 256 stays exact in fp32 and bf16
-      // range); the normalisation by l is unaffected.
       const bool grow = mx > m_run[qt] + kLazyRescaleLog2;
       const float mn = grow ? mx : m_run[qt];
       alpha[qt] = grow ? ((m_run[qt] == -INFINITY) ? 0.f : fast_exp2(m_run[qt] - mn)) : 1.0f;
       m_run[qt] = mn;
       any_rescale |= grow;
     }
-#pragma unroll
-    for (int qt = 0; qt < C::QT; ++qt) {
-      // every key so far masked (a walk that starts past some rows'
-      // positions: group B's first block, or a key run, over a cached prefix
-      // not aligned to the blocks): p = 0, not exp2(-inf + inf)
-      const float nm = (m_run[qt] == -INFINITY) ? 0.f : -m_run[qt];
-#pragma unroll
-      for (int s2 = 0; s2 < C::PS; ++s2) {
-        float p[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          p[j] = fast_exp2(fmaf(st[2 * s2][qt][j], scale_log2, nm));
-          p[4 + j] = fast_exp2(fmaf(st[2 * s2 + 1][qt][j], scale_log2, nm));
-        }
-        const u32x4 w = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                         pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])};
-        pb[s2][qt] = as_bf16x8(w);
-      }
-    }
     // o_acc and l hold every block before j (M(j) added P_{j-1}).
     if (__any(any_rescale)) {
+      exp_pass();
 #pragma unroll
       for (int qt = 0; qt < C::QT; ++qt) {
         l_run[qt] *= alpha[qt];
